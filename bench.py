@@ -1,0 +1,234 @@
+#!/usr/bin/env python3
+"""MoE decode tok/s (bs=1, 48 layers) + achieved HBM GB/s of the
+gather-dequant-GEMV kernels against the MI355X peak.
+
+Workload (default): a 48-layer stack of Qwen3-30B-A3B-shaped MoE blocks (128
+experts, hidden 2048, expert 768, top-8, 4-bit affine group 64), no
+attention, bs=1 decode of 64 consecutive tokens; a 3072-slot HBM pool over the
+6144 (layer, expert) pairs with the HBM expert store behind it; router logits
+biased by a Zipf(1.1) per-layer popularity; residual h += 0.1*N(0,1) per
+layer.  One step = the 64 tokens.  Synthetic seeded weights and inputs.
+
+Prints ONE JSON line (rank 0).  `--gpus N` with N > 1 is refused: this build
+measures one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0   # MI355X HBM3E, 8 TB/s
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--tokens", type=int, default=64)
+    ap.add_argument("--workload", default="qwen3-48l",
+                    choices=["qwen3-48l", "gptoss-36l"])
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile-tokens", type=int, default=8,
+                    help="tokens of the kernel-timing pass after the timed steps")
+    return ap.parse_args()
+
+
+def workload(args, device):
+    from moe_stream_amd import geometry as G
+    from moe_stream_amd.stack import DecodeStack
+    if args.workload == "qwen3-48l":
+        geom, L, slots = G.QWEN3_30B_A3B, 48, 3072
+        stack = DecodeStack(geom, L, slots, device, zipf_s=1.1)
+        cfg = {"workload": "qwen3-30b-a3b-moe-stack", "layers": L, "experts": 128,
+               "d_model": 2048, "d_ff": 768, "top_k": 8, "pool_slots": slots,
+               "pairs": L * 128, "quant": "4-bit affine g64, bf16 scales/biases",
+               "router_bias": "zipf(1.1) log-popularity", "global_batch": 1,
+               "tokens_per_step": args.tokens}
+    else:
+        geom, L, slots = G.GPT_OSS_120B, 36, 2304
+        stack = DecodeStack(geom, L, slots, device, zipf_s=None, router_bias=True)
+        cfg = {"workload": "gpt-oss-120b-moe-stack", "layers": L, "experts": 128,
+               "d_model": 2880, "d_ff": 2880, "top_k": 4, "pool_slots": slots,
+               "pairs": L * 128, "quant": "4-bit affine g64 + bf16 proj bias",
+               "activation": "clamped swiglu a=1.702 limit=7", "global_batch": 1,
+               "tokens_per_step": args.tokens}
+    return stack, cfg
+
+
+def time_dominant_kernel(stack, xs, n_tok):
+    """Average duration of the gate/up dequant-GEMV kernel, each launch
+    bracketed by HIP events on the stream it runs on."""
+    import torch
+    from moe_stream_amd import _lib, ops
+    L = _lib.lib()
+    g = stack.geom.c_geom()
+    view = stack.pool.c_view()
+    s = torch.cuda.current_stream()
+    sp = _lib.stream_ptr(s)
+    pairs = []
+    for t in range(n_tok):
+        stack.x_in.copy_(xs[t])
+        for Lx in range(stack.L):
+            nxt = Lx + 1 < stack.L
+            b = stack.bias[Lx] if stack.bias is not None else None
+            bn = stack.bias[Lx + 1] if (stack.bias is not None and nxt) else None
+            bufs = stack.bufs[Lx]
+            ops.route(stack.x_in[Lx:Lx + 1], stack.W[Lx], b, stack.geom.routing,
+                      stack.geom.norm_topk_prob, stack.k,
+                      W_next=stack.W[Lx + 1] if nxt else None, bias_next=bn,
+                      k_pred=stack.k_pred, table=stack.table[Lx], bufs=bufs,
+                      workspace=stack.route_ws)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            _lib.check(L.moe_ffn_decode_up(C.byref(view), C.byref(g),
+                                           bufs.slot_refs.data_ptr(),
+                                           stack.x_in[Lx:Lx + 1].data_ptr(), 1, stack.k,
+                                           stack.ffn_ws.data_ptr(), stack.ffn_ws.numel(), sp))
+            e1.record(s)
+            _lib.check(L.moe_ffn_decode_down(C.byref(view), C.byref(g),
+                                             bufs.slot_refs.data_ptr(),
+                                             bufs.scores.data_ptr(), 1, stack.k,
+                                             stack.y[Lx:Lx + 1].data_ptr(), None,
+                                             stack.ffn_ws.data_ptr(), stack.ffn_ws.numel(), sp))
+            pairs.append((e0, e1))
+    torch.cuda.synchronize()
+    ms = [a.elapsed_time(b) for a, b in pairs]
+    return float(np.mean(ms)), float(np.median(ms)), len(ms)
+
+
+def cpu_baseline(stack, xs, seconds):
+    """The oracle (numpy port of the reference graph) on the host cores:
+    router + top-k + the k-expert block per layer, fp64, BLAS held to one
+    thread.  Bounded sample: consecutive layers of the first tokens until
+    `seconds` of work; rate scaled to tokens/s of the full stack."""
+    import torch
+    from threadpoolctl import threadpool_limits
+    from oracle import layout as OL
+    from oracle import numerics as N
+    g = stack.geom
+    kind = "qwen3" if not g.has_proj_bias else "gptoss"
+    W = stack.W.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    B = None if stack.bias is None else stack.bias.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    xh = xs.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    cache = {}
+
+    def expert(Lx, e):
+        key = (Lx, e)
+        if key not in cache:
+            rec = stack.store[Lx * stack.E + e].cpu().numpy()
+            cache[key] = OL.split_record(rec, g.d_model, g.d_ff, g.has_proj_bias)
+        return cache[key]
+
+    done, t_work = 0, 0.0
+    with threadpool_limits(limits=1):
+        t, Lx = 0, 0
+        while t_work < seconds and done < 4 * stack.L:
+            x = N.bf16_bits_to_f32(xh[t, Lx]).astype(np.float64)
+            exps = None
+            # fetch the routed experts' bytes first (not timed: the reference
+            # reads them from its resident pool)
+            z0 = N.router_logits(x, W[Lx], None if B is None else B[Lx], "mlx")
+            ids0 = (N.top_k_experts(z0, g.top_k, g.norm_topk_prob, "mlx")[0]
+                    if g.routing == 0 else N.top_k_route(z0, g.top_k, "mlx")[0])
+            exps = [expert(Lx, int(e)) for e in ids0]
+            t0 = time.perf_counter()
+            z = N.router_logits(x, W[Lx], None if B is None else B[Lx], "mlx")
+            if g.routing == 0:
+                ids, sc, _ = N.top_k_experts(z, g.top_k, g.norm_topk_prob, "mlx")
+            else:
+                ids, sc, _ = N.top_k_route(z, g.top_k, "mlx")
+            N.moe_block(x, exps, sc, kind=kind, mode="mlx")
+            t_work += time.perf_counter() - t0
+            done += 1
+            Lx += 1
+            if Lx == stack.L:
+                Lx, t = 0, t + 1
+    per_layer = t_work / done
+    return {"value": 1.0 / (per_layer * stack.L), "unit": "tok/s", "cores": 1,
+            "kind": "port",
+            "sample": f"{done} layer-blocks (router+top-k+{g.top_k} experts, numpy fp64 "
+                      f"MLX-emulation oracle, BLAS 1 thread) of the same stack, "
+                      f"{t_work:.1f} s of CPU work; host has {os.cpu_count()} cpus"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the expert path at bs=1 does not shard "
+              "(see the sharding note in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from moe_stream_amd import synth
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stack, cfg = workload(args, dev)
+    xs = synth.hidden_states(args.tokens, stack.L, stack.geom.d_model, dev,
+                             synth.SEED_BASE + 200)
+    use_graph = not args.no_graph
+    if use_graph:
+        stack.capture()
+    torch.cuda.synchronize()
+
+    def step():
+        for t in range(args.tokens):
+            stack.run_token(xs[t], use_graph)
+
+    for _ in range(args.warmup):
+        step()
+    for b in stack.bufs:
+        b.miss.zero_()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = e0.elapsed_time(e1)
+    ms_per_step = gpu_ms / args.steps
+    tok_s = args.tokens * args.steps / (gpu_ms / 1e3)
+    misses = int(sum(int(b.miss.item()) for b in stack.bufs))
+    lookups = args.steps * args.tokens * stack.L * stack.k
+    cfg["pool_hit_rate"] = round(1.0 - misses / lookups, 4)
+    cfg["graph"] = use_graph
+    cfg["parallelism"] = "none (1 GPU)"
+    cfg["seq_len"] = 1
+
+    # roofline of the dominant kernel (gate/up dequant-GEMV)
+    up_bytes = stack.k * sum(c.nbytes for c in stack.geom.components
+                             if c.name.startswith(("gate_proj", "up_proj")))
+    avg_ms, med_ms, n = time_dominant_kernel(stack, xs, min(args.profile_tokens, args.tokens))
+    achieved = up_bytes / (avg_ms * 1e-3) / 1e9
+    roof = {"bound": "hbm", "kernel": "ffn_gate_up_kernel", "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None, "bytes_per_launch": up_bytes,
+            "avg_us": round(avg_ms * 1e3, 3), "median_us": round(med_ms * 1e3, 3),
+            "launches": n}
+    block_bytes = stack.expert_bytes_per_token()
+    out = {"metric": "MoE decode tok/s (bs=1, 48 layers) + gather_qmm achieved HBM GB/s vs peak",
+           "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "bf16", "data": "synthetic",
+           "config": cfg, "roofline": roof,
+           "expert_bytes_per_token": block_bytes,
+           "stack_expert_GBs": round(block_bytes * tok_s / 1e9, 1),
+           "wall_s": round(wall, 3)}
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(stack, xs, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

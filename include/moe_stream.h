@@ -1,0 +1,195 @@
+/*
+ * moe_stream.h -- C ABI of the MI355X expert hot path of moe-stream.
+ *
+ * Plain C: device pointers, sizes and a hipStream_t (passed as void*).  No
+ * exceptions cross this boundary; every entry point returns an int status
+ * (MOE_OK = 0, negative on error) and moe_last_error() describes the last
+ * failure of the calling thread.  All buffers are owned by the caller (the
+ * convention of the reference's array_from_ptr, ext/src/zerocopy.cpp:76-97).
+ * Calls on one stream are ordered by that stream; the caller serialises
+ * calls that share a workspace.
+ *
+ * bf16 values are passed as uint16_t bit patterns; 4-bit codes as uint32_t
+ * words, element i of a row in word i>>3 at bit 4*(i&7) (low nibble first).
+ */
+#ifndef MOE_STREAM_H
+#define MOE_STREAM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MOE_OK = 0,
+  MOE_ERR_INVALID = -1,     /* bad argument (null, size, alignment, range) */
+  MOE_ERR_UNSUPPORTED = -2, /* geometry with no compiled kernel            */
+  MOE_ERR_HIP = -3,         /* the HIP runtime reported an error           */
+  MOE_ERR_EXHAUSTED = -4,   /* slot pool exhausted (every slot pinned)     */
+  MOE_ERR_DEVICE = -5       /* a kernel flagged an out-of-range slot ref   */
+};
+
+/* Gated activation between gate/up and down. */
+enum { MOE_ACT_SWIGLU = 0, MOE_ACT_SWIGLU_CLAMP = 1 };
+
+/* Routing rule. */
+enum {
+  MOE_ROUTE_SOFTMAX_TOPK = 0, /* softmax over E, top-k, optional renorm (Qwen3)   */
+  MOE_ROUTE_TOPK_SOFTMAX = 1  /* top-k of raw logits, softmax over the k (gpt-oss) */
+};
+
+#define MOE_MAX_COMPONENTS 12
+#define MOE_MAX_TOPK 16
+
+/* Expert geometry.  d_model = hidden size D, d_ff = expert intermediate F. */
+typedef struct moe_geom {
+  int32_t d_model;
+  int32_t d_ff;
+  int32_t group_size;    /* 64 */
+  int32_t bits;          /* 4  */
+  int32_t has_proj_bias; /* 1 for gpt-oss: each projection adds a bf16 bias  */
+  int32_t act;           /* MOE_ACT_*                                        */
+  float alpha;           /* clamped SwiGLU alpha (1.702)                     */
+  float limit;           /* clamped SwiGLU limit (7.0)                       */
+} moe_geom;
+
+/*
+ * The slot pool as the kernels see it: one array per component shaped
+ * [n_slots, *shape] (the reference's layout, engine_v3.py:180-206), plus an
+ * optional expert store in the repacked record layout (repack.py:73-82,141):
+ * record r at store + r*record_bytes, component c at comp_offset[c] in it.
+ *
+ * Component order: proj-major over (gate_proj, up_proj, down_proj), then
+ * part over (weight, scales, biases[, bias]) -- 9 components, or 12 when
+ * has_proj_bias.
+ *
+ * A slot reference is an int32: ref >= 0 names pool slot `ref`; ref < 0
+ * names store record (-ref - 1).
+ */
+typedef struct moe_pool_view {
+  int32_t n_components;
+  int32_t n_slots;
+  void *base[MOE_MAX_COMPONENTS];
+  int64_t slot_bytes[MOE_MAX_COMPONENTS];
+  const void *store;
+  int64_t record_bytes;
+  int64_t n_records;
+  int64_t comp_offset[MOE_MAX_COMPONENTS];
+} moe_pool_view;
+
+/* Library identity and error reporting. */
+int moe_version(void);
+const char *moe_last_error(void);
+
+/* Bytes of the components of one expert for a geometry: writes up to 12
+ * component sizes and returns the number of components (or < 0). */
+int moe_component_bytes(const moe_geom *g, int64_t *bytes_out);
+
+/*
+ * Batch-1 (small T) expert block: for each token t and routed expert j,
+ *   y_t = sum_j scores[t*k+j] * down_j( act(gate_j(x_t), up_j(x_t)) )
+ * read from the pool/store via slot_refs[t*k+j].  Dequant, gate/up, the
+ * activation, down and the weighted combine are fused into two kernels; the
+ * [T*k, d_ff] intermediate never leaves the workspace.  fp32 accumulation.
+ *
+ * Replaces the three mx.gather_qmm calls + swiglu + weighted sum of
+ * engine_v3.py:588-600 (Qwen3) and engine_120b.py:132-145 (gpt-oss), and the
+ * disabled fused Metal kernel kernels.moe_expert_mlp (kernels.py:231-252).
+ *
+ * x: bf16 [T, d_model]; out_bf16: bf16 [T, d_model] (may be NULL);
+ * out_f32: fp32 [T, d_model] (may be NULL; debug output).
+ * workspace: device memory of at least moe_ffn_decode_workspace() bytes.
+ */
+size_t moe_ffn_decode_workspace(const moe_geom *g, int32_t T, int32_t k);
+int moe_ffn_decode(const moe_pool_view *pool, const moe_geom *g,
+                   const int32_t *slot_refs, const float *scores,
+                   const uint16_t *x, int32_t T, int32_t k,
+                   uint16_t *out_bf16, float *out_f32,
+                   void *workspace, size_t workspace_bytes, void *stream);
+
+/* The two halves of moe_ffn_decode, for callers that time or schedule them
+ * separately: _up writes the bf16 [T*k, d_ff] activations into the
+ * workspace, _down reads them (same workspace) and writes the combined
+ * output.  moe_ffn_decode == _up then _down on one stream. */
+int moe_ffn_decode_up(const moe_pool_view *pool, const moe_geom *g,
+                      const int32_t *slot_refs, const uint16_t *x, int32_t T,
+                      int32_t k, void *workspace, size_t workspace_bytes,
+                      void *stream);
+int moe_ffn_decode_down(const moe_pool_view *pool, const moe_geom *g,
+                        const int32_t *slot_refs, const float *scores,
+                        int32_t T, int32_t k, uint16_t *out_bf16,
+                        float *out_f32, void *workspace,
+                        size_t workspace_bytes, void *stream);
+
+/*
+ * Router + top-k (+ lookahead + slot lookup) for T tokens in one launch.
+ *   logits = x @ W.T (+ bias), materialised as bf16;
+ *   mode SOFTMAX_TOPK: probs = bf16(softmax(logits)); top-k of probs; scores
+ *     = probs (renormalised, in bf16 steps, when renorm != 0)
+ *     (top_k_experts, engine_v3.py:467-473);
+ *   mode TOPK_SOFTMAX: top-k of logits; scores = bf16(softmax(selected))
+ *     (top_k_route, engine_120b.py:65-70).
+ * ids are ranked (value descending, ties to the lower expert id).
+ * Lookahead (W_next != NULL): pred_ids[t, 0..k_pred) = top-k_pred of the raw
+ *   bf16 logits of x @ W_next.T (+ bias_next) (top_k_indices,
+ *   engine_v3.py:476-483, engine_120b.py:73-75).
+ * Slot lookup (table != NULL): slot_refs[t*k+j] = table[ids[t*k+j]], the
+ *   device mirror of ExpertPool.slot_of for this layer (engine_v3.py:215);
+ *   *miss_count (if not NULL) is incremented by the number of refs < 0.
+ * scores are fp32 holding bf16-representable values.
+ * workspace: at least moe_route_workspace() bytes, zeroed once before first
+ * use (the kernel leaves its counter at zero when it returns).
+ */
+size_t moe_route_workspace(int32_t T, int32_t E);
+int moe_route(const uint16_t *x, int32_t T, int32_t d_model,
+              const uint16_t *W, const uint16_t *bias, int32_t E,
+              int32_t mode, int32_t renorm, int32_t k,
+              int32_t *ids, float *scores,
+              const uint16_t *W_next, const uint16_t *bias_next,
+              int32_t k_pred, int32_t *pred_ids,
+              const int32_t *table, int32_t *slot_refs, int32_t *miss_count,
+              void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Device-side (layer, expert) -> slot lookup for n ids (the index build of
+ * engine_v3.py:550-552 against the slot table of engine_v3.py:215):
+ * slot_refs[i] = table[ids[i]] for ids in [0, E); out-of-range ids give
+ * MOE_ERR_DEVICE through the flag in *miss_count's sibling error word.
+ */
+int moe_slot_lookup(const int32_t *table, int32_t E, const int32_t *ids,
+                    int32_t n, int32_t *slot_refs, int32_t *miss_count,
+                    void *stream);
+
+/* Slot fills: copy n whole expert records into pool slots.
+ * src_records: record indices into `src_store` (host pinned or device
+ * memory laid out like pool->store; NULL means pool->store), dst_slots: pool
+ * slots.  Host index arrays.  Enqueued on `stream` (hipMemcpyAsync per
+ * component).  Replaces ExpertPool._read (engine_v3.py:255-290). */
+int moe_fill_slots(const moe_pool_view *pool, const void *src_store,
+                   int64_t src_record_bytes, const int64_t *src_records,
+                   const int32_t *dst_slots, int32_t n, void *stream);
+
+/* Pinned host memory for the expert store (hipHostMalloc). */
+int moe_host_alloc(size_t bytes, void **out);
+int moe_host_free(void *p);
+
+/* Events for stream-ordered slot reuse (the role of needs_barrier,
+ * engine_v3.py:228-231, 601-607). */
+int moe_event_create(void **ev);
+int moe_event_destroy(void *ev);
+int moe_event_record(void *ev, void *stream);
+int moe_event_query(void *ev);                 /* 1 done, 0 pending, <0 err */
+int moe_stream_wait_event(void *stream, void *ev);
+int moe_event_elapsed_ms(void *start, void *stop, float *ms);
+
+/* Read and clear the device error word set by the kernels (out-of-range slot
+ * refs), synchronising `stream`.  Returns MOE_OK or MOE_ERR_DEVICE. */
+int moe_check_device_error(void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOE_STREAM_H */

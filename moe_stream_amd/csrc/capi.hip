@@ -1,0 +1,389 @@
+// C ABI of the expert hot path: argument checks, geometry dispatch, slot
+// fills, pinned host memory and events.  No exceptions cross this boundary;
+// failures return a negative status and set a thread-local message.
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "launchers.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+  return fail(MOE_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define MOE_HIP(call)                                   \
+  do {                                                  \
+    hipError_t e_ = (call);                             \
+    if (e_ != hipSuccess) return hip_fail(e_, #call);   \
+  } while (0)
+
+bool aligned(const void *p, size_t a) {
+  return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+// Component sizes of one expert: proj-major (gate, up, down) x part-major
+// (weight, scales, biases[, bias]); the order of repack.py:35-37 and
+// repack_gptoss.py:54-55.
+int component_bytes(const moe_geom *g, int64_t *b) {
+  if (!g) return fail(MOE_ERR_INVALID, "geom is NULL");
+  if (g->group_size != 64 || g->bits != 4)
+    return fail(MOE_ERR_UNSUPPORTED, "only 4-bit affine, group 64 (got %d-bit, group %d)",
+                g->bits, g->group_size);
+  if (g->d_model <= 0 || g->d_ff <= 0 || g->d_model % 64 || g->d_ff % 64)
+    return fail(MOE_ERR_INVALID, "d_model=%d d_ff=%d must be positive multiples of 64",
+                g->d_model, g->d_ff);
+  const int np = g->has_proj_bias ? 4 : 3;
+  const int64_t D = g->d_model, F = g->d_ff;
+  for (int p = 0; p < 3; ++p) {
+    const int64_t out = (p == 2) ? D : F, in = (p == 2) ? F : D;
+    b[p * np + 0] = out * in / 2;          // uint32 codes, 8 per word
+    b[p * np + 1] = out * (in / 64) * 2;   // bf16 scales
+    b[p * np + 2] = out * (in / 64) * 2;   // bf16 biases
+    if (np == 4) b[p * np + 3] = out * 2;  // bf16 projection bias
+  }
+  return np * 3;
+}
+
+int make_pool_args(const moe_pool_view *v, const moe_geom *g, moe::PoolArgs *pa) {
+  if (!v) return fail(MOE_ERR_INVALID, "pool view is NULL");
+  int64_t cb[MOE_MAX_COMPONENTS];
+  const int nc = component_bytes(g, cb);
+  if (nc < 0) return nc;
+  if (v->n_components != nc)
+    return fail(MOE_ERR_INVALID, "pool view has %d components, geometry needs %d",
+                v->n_components, nc);
+  if (v->n_slots < 0) return fail(MOE_ERR_INVALID, "n_slots < 0");
+  const int np = nc / 3;
+  for (int c = 0; c < nc; ++c) {
+    const size_t align = (c % np == 0) ? 16 : 2;
+    if (v->n_slots > 0) {
+      if (!v->base[c]) return fail(MOE_ERR_INVALID, "component %d base is NULL", c);
+      if (!aligned(v->base[c], align) || v->slot_bytes[c] % (int64_t)align)
+        return fail(MOE_ERR_INVALID, "component %d misaligned for %zu-byte loads", c, align);
+      if (v->slot_bytes[c] < cb[c])
+        return fail(MOE_ERR_INVALID, "component %d slot stride %lld < %lld bytes", c,
+                    (long long)v->slot_bytes[c], (long long)cb[c]);
+    }
+    pa->base[c] = static_cast<const char *>(v->base[c]);
+    pa->slot_bytes[c] = v->slot_bytes[c];
+    pa->comp_offset[c] = v->comp_offset[c];
+    if (v->store) {
+      if (v->comp_offset[c] < 0 || v->comp_offset[c] + cb[c] > v->record_bytes)
+        return fail(MOE_ERR_INVALID, "component %d [%lld,+%lld) outside the %lld-byte record",
+                    c, (long long)v->comp_offset[c], (long long)cb[c],
+                    (long long)v->record_bytes);
+      if (v->comp_offset[c] % (int64_t)align)
+        return fail(MOE_ERR_INVALID, "component %d store offset misaligned", c);
+    }
+  }
+  for (int c = nc; c < MOE_MAX_COMPONENTS; ++c) {
+    pa->base[c] = nullptr;
+    pa->slot_bytes[c] = 0;
+    pa->comp_offset[c] = 0;
+  }
+  pa->store = static_cast<const char *>(v->store);
+  pa->record_bytes = v->record_bytes;
+  if (v->store && (!aligned(v->store, 16) || v->record_bytes % 16))
+    return fail(MOE_ERR_INVALID, "store base/record size must be 16-byte aligned");
+  if (v->n_records > INT32_MAX) return fail(MOE_ERR_INVALID, "too many store records");
+  pa->n_records = v->store ? (int32_t)v->n_records : 0;
+  pa->n_slots = v->n_slots;
+  return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_version(void) { return 1; }
+
+const char *moe_last_error(void) { return g_err.c_str(); }
+
+int moe_component_bytes(const moe_geom *g, int64_t *bytes_out) {
+  if (!bytes_out) return fail(MOE_ERR_INVALID, "bytes_out is NULL");
+  return component_bytes(g, bytes_out);
+}
+
+size_t moe_ffn_decode_workspace(const moe_geom *g, int32_t T, int32_t k) {
+  if (!g || T <= 0 || k <= 0) return 0;
+  // h: bf16 [T*k, d_ff], padded to 256 bytes
+  const size_t h = (size_t)T * k * g->d_ff * 2;
+  return (h + 255) & ~(size_t)255;
+}
+
+// Shared argument checks of the decode entry points.
+static int ffn_prepare(const moe_pool_view *pool, const moe_geom *g,
+                       const int32_t *slot_refs, int32_t T, int32_t k,
+                       void *workspace, size_t workspace_bytes,
+                       moe::PoolArgs *pa, const moe::FfnLaunch **L) {
+  int rc = make_pool_args(pool, g, pa);
+  if (rc) return rc;
+  if (T <= 0) return fail(MOE_ERR_INVALID, "T=%d must be positive", T);
+  if (k <= 0 || k > MOE_MAX_TOPK)
+    return fail(MOE_ERR_INVALID, "k=%d outside [1, %d]", k, MOE_MAX_TOPK);
+  if (!slot_refs || !workspace) return fail(MOE_ERR_INVALID, "NULL slot_refs/workspace");
+  if (!aligned(workspace, 16)) return fail(MOE_ERR_INVALID, "workspace misaligned");
+  if (workspace_bytes < moe_ffn_decode_workspace(g, T, k))
+    return fail(MOE_ERR_INVALID, "workspace %zu < %zu bytes", workspace_bytes,
+                moe_ffn_decode_workspace(g, T, k));
+  if (g->act != MOE_ACT_SWIGLU && g->act != MOE_ACT_SWIGLU_CLAMP)
+    return fail(MOE_ERR_INVALID, "unknown activation %d", g->act);
+  *L = moe::find_ffn(g->d_model, g->d_ff, g->has_proj_bias);
+  if (!*L)
+    return fail(MOE_ERR_UNSUPPORTED,
+                "no decode kernel compiled for d_model=%d d_ff=%d proj_bias=%d",
+                g->d_model, g->d_ff, g->has_proj_bias);
+  return MOE_OK;
+}
+
+int moe_ffn_decode_up(const moe_pool_view *pool, const moe_geom *g,
+                      const int32_t *slot_refs, const uint16_t *x, int32_t T,
+                      int32_t k, void *workspace, size_t workspace_bytes,
+                      void *stream) {
+  moe::PoolArgs pa;
+  const moe::FfnLaunch *L = nullptr;
+  int rc = ffn_prepare(pool, g, slot_refs, T, k, workspace, workspace_bytes, &pa, &L);
+  if (rc) return rc;
+  if (!x) return fail(MOE_ERR_INVALID, "NULL x");
+  if (!aligned(x, 16)) return fail(MOE_ERR_INVALID, "x must be 16-byte aligned");
+  (void)hipGetLastError();
+  moe::launch_ffn_up(L, pa, slot_refs, x, T, k, static_cast<uint16_t *>(workspace),
+                     g->act, g->alpha, g->limit, static_cast<hipStream_t>(stream));
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+int moe_ffn_decode_down(const moe_pool_view *pool, const moe_geom *g,
+                        const int32_t *slot_refs, const float *scores,
+                        int32_t T, int32_t k, uint16_t *out_bf16,
+                        float *out_f32, void *workspace,
+                        size_t workspace_bytes, void *stream) {
+  moe::PoolArgs pa;
+  const moe::FfnLaunch *L = nullptr;
+  int rc = ffn_prepare(pool, g, slot_refs, T, k, workspace, workspace_bytes, &pa, &L);
+  if (rc) return rc;
+  if (!scores) return fail(MOE_ERR_INVALID, "NULL scores");
+  if (!out_bf16 && !out_f32) return fail(MOE_ERR_INVALID, "no output buffer");
+  (void)hipGetLastError();
+  moe::launch_ffn_down(L, pa, slot_refs, scores, T, k,
+                       static_cast<const uint16_t *>(workspace), out_bf16, out_f32,
+                       static_cast<hipStream_t>(stream));
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+int moe_ffn_decode(const moe_pool_view *pool, const moe_geom *g,
+                   const int32_t *slot_refs, const float *scores,
+                   const uint16_t *x, int32_t T, int32_t k, uint16_t *out_bf16,
+                   float *out_f32, void *workspace, size_t workspace_bytes,
+                   void *stream) {
+  moe::PoolArgs pa;
+  const moe::FfnLaunch *L = nullptr;
+  int rc = ffn_prepare(pool, g, slot_refs, T, k, workspace, workspace_bytes, &pa, &L);
+  if (rc) return rc;
+  if (!scores || !x) return fail(MOE_ERR_INVALID, "NULL scores/x");
+  if (!out_bf16 && !out_f32) return fail(MOE_ERR_INVALID, "no output buffer");
+  if (!aligned(x, 16)) return fail(MOE_ERR_INVALID, "x must be 16-byte aligned");
+  (void)hipGetLastError();
+  moe::launch_ffn_decode(L, pa, slot_refs, scores, x, T, k,
+                         static_cast<uint16_t *>(workspace), out_bf16, out_f32,
+                         g->act, g->alpha, g->limit,
+                         static_cast<hipStream_t>(stream));
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+size_t moe_route_workspace(int32_t T, int32_t E) {
+  if (T <= 0 || E <= 0) return 0;
+  // counter word (padded to 256 B) + logits [2][T][E] fp32
+  return 256 + (((size_t)2 * T * E * 4 + 255) & ~(size_t)255);
+}
+
+int moe_route(const uint16_t *x, int32_t T, int32_t d_model, const uint16_t *W,
+              const uint16_t *bias, int32_t E, int32_t mode, int32_t renorm,
+              int32_t k, int32_t *ids, float *scores, const uint16_t *W_next,
+              const uint16_t *bias_next, int32_t k_pred, int32_t *pred_ids,
+              const int32_t *table, int32_t *slot_refs, int32_t *miss_count,
+              void *workspace, size_t workspace_bytes, void *stream) {
+  if (T <= 0 || T > moe::kRouteMaxT)
+    return fail(MOE_ERR_INVALID, "T=%d outside [1, %d]", T, moe::kRouteMaxT);
+  if (E <= 0 || E > moe::kRouteMaxE)
+    return fail(MOE_ERR_INVALID, "E=%d outside [1, %d]", E, moe::kRouteMaxE);
+  if (d_model <= 0 || d_model % 8)
+    return fail(MOE_ERR_INVALID, "d_model=%d must be a positive multiple of 8", d_model);
+  if (k <= 0 || k > MOE_MAX_TOPK || k > E)
+    return fail(MOE_ERR_INVALID, "k=%d outside [1, min(E, %d)]", k, MOE_MAX_TOPK);
+  if (mode != MOE_ROUTE_SOFTMAX_TOPK && mode != MOE_ROUTE_TOPK_SOFTMAX)
+    return fail(MOE_ERR_INVALID, "unknown routing mode %d", mode);
+  if (!x || !W || !ids || !scores || !workspace)
+    return fail(MOE_ERR_INVALID, "NULL x/W/ids/scores/workspace");
+  if (!aligned(x, 16) || !aligned(W, 16))
+    return fail(MOE_ERR_INVALID, "x and W must be 16-byte aligned");
+  if (W_next) {
+    if (!pred_ids) return fail(MOE_ERR_INVALID, "W_next given without pred_ids");
+    if (k_pred <= 0 || k_pred > E)
+      return fail(MOE_ERR_INVALID, "k_pred=%d outside [1, E]", k_pred);
+    if (!aligned(W_next, 16)) return fail(MOE_ERR_INVALID, "W_next misaligned");
+  }
+  if (table && !slot_refs) return fail(MOE_ERR_INVALID, "table given without slot_refs");
+  if (workspace_bytes < moe_route_workspace(T, E))
+    return fail(MOE_ERR_INVALID, "workspace %zu < %zu bytes", workspace_bytes,
+                moe_route_workspace(T, E));
+  if (!aligned(workspace, 256)) return fail(MOE_ERR_INVALID, "workspace misaligned");
+  moe::RouteArgs a;
+  a.x = x;
+  a.W = W;
+  a.bias = bias;
+  a.Wn = W_next;
+  a.bias_n = W_next ? bias_next : nullptr;
+  a.ids = ids;
+  a.scores = scores;
+  a.pred = pred_ids;
+  a.table = table;
+  a.slot_refs = slot_refs;
+  a.miss_count = miss_count;
+  a.counter = static_cast<uint32_t *>(workspace);
+  a.logits = reinterpret_cast<float *>(static_cast<char *>(workspace) + 256);
+  a.T = T;
+  a.D = d_model;
+  a.E = E;
+  a.mode = mode;
+  a.renorm = renorm;
+  a.k = k;
+  a.kp = W_next ? k_pred : 0;
+  (void)hipGetLastError();
+  moe::launch_route(a, static_cast<hipStream_t>(stream));
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+int moe_slot_lookup(const int32_t *table, int32_t E, const int32_t *ids,
+                    int32_t n, int32_t *slot_refs, int32_t *miss_count,
+                    void *stream) {
+  if (n < 0 || E <= 0) return fail(MOE_ERR_INVALID, "n=%d E=%d", n, E);
+  if (n == 0) return MOE_OK;
+  if (!table || !ids || !slot_refs)
+    return fail(MOE_ERR_INVALID, "NULL table/ids/slot_refs");
+  (void)hipGetLastError();
+  moe::launch_slot_lookup(table, E, ids, n, slot_refs, miss_count,
+                          static_cast<hipStream_t>(stream));
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+int moe_fill_slots(const moe_pool_view *pool, const void *src_store,
+                   int64_t src_record_bytes, const int64_t *src_records,
+                   const int32_t *dst_slots, int32_t n, void *stream) {
+  if (!pool) return fail(MOE_ERR_INVALID, "pool view is NULL");
+  if (n < 0) return fail(MOE_ERR_INVALID, "n < 0");
+  if (n == 0) return MOE_OK;
+  if (!src_records || !dst_slots) return fail(MOE_ERR_INVALID, "NULL index arrays");
+  const char *src = static_cast<const char *>(src_store ? src_store : pool->store);
+  const int64_t rb = src_store ? src_record_bytes : pool->record_bytes;
+  if (!src || rb <= 0) return fail(MOE_ERR_INVALID, "no source store");
+  const int nc = pool->n_components;
+  if (nc != 9 && nc != 12) return fail(MOE_ERR_INVALID, "n_components=%d", nc);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  for (int32_t i = 0; i < n; ++i) {
+    const int32_t slot = dst_slots[i];
+    const int64_t rec = src_records[i];
+    if (slot < 0 || slot >= pool->n_slots)
+      return fail(MOE_ERR_INVALID, "slot %d outside [0, %d)", slot, pool->n_slots);
+    if (rec < 0 || (!src_store && rec >= pool->n_records))
+      return fail(MOE_ERR_INVALID, "record %lld out of range", (long long)rec);
+    for (int c = 0; c < nc; ++c) {
+      // each component's size is its slot stride in the pool
+      MOE_HIP(hipMemcpyAsync(static_cast<char *>(pool->base[c]) + slot * pool->slot_bytes[c],
+                             src + rec * rb + pool->comp_offset[c],
+                             (size_t)pool->slot_bytes[c], hipMemcpyDefault, s));
+    }
+  }
+  return MOE_OK;
+}
+
+int moe_host_alloc(size_t bytes, void **out) {
+  if (!out) return fail(MOE_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  if (bytes == 0) return fail(MOE_ERR_INVALID, "zero-byte allocation");
+  MOE_HIP(hipHostMalloc(out, bytes, hipHostMallocDefault));
+  return MOE_OK;
+}
+
+int moe_host_free(void *p) {
+  if (!p) return MOE_OK;
+  MOE_HIP(hipHostFree(p));
+  return MOE_OK;
+}
+
+int moe_event_create(void **ev) {
+  if (!ev) return fail(MOE_ERR_INVALID, "ev is NULL");
+  hipEvent_t e;
+  MOE_HIP(hipEventCreateWithFlags(&e, hipEventDefault));
+  *ev = e;
+  return MOE_OK;
+}
+
+int moe_event_destroy(void *ev) {
+  if (!ev) return MOE_OK;
+  MOE_HIP(hipEventDestroy(static_cast<hipEvent_t>(ev)));
+  return MOE_OK;
+}
+
+int moe_event_record(void *ev, void *stream) {
+  if (!ev) return fail(MOE_ERR_INVALID, "ev is NULL");
+  MOE_HIP(hipEventRecord(static_cast<hipEvent_t>(ev), static_cast<hipStream_t>(stream)));
+  return MOE_OK;
+}
+
+int moe_event_query(void *ev) {
+  if (!ev) return fail(MOE_ERR_INVALID, "ev is NULL");
+  hipError_t e = hipEventQuery(static_cast<hipEvent_t>(ev));
+  if (e == hipSuccess) return 1;
+  if (e == hipErrorNotReady) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return hip_fail(e, "hipEventQuery");
+}
+
+int moe_stream_wait_event(void *stream, void *ev) {
+  if (!ev) return fail(MOE_ERR_INVALID, "ev is NULL");
+  MOE_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(ev), 0));
+  return MOE_OK;
+}
+
+int moe_event_elapsed_ms(void *start, void *stop, float *ms) {
+  if (!start || !stop || !ms) return fail(MOE_ERR_INVALID, "NULL argument");
+  MOE_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)));
+  return MOE_OK;
+}
+
+int moe_check_device_error(void *stream) {
+  MOE_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+  int v = 0;
+  MOE_HIP(hipMemcpyFromSymbol(&v, HIP_SYMBOL(moe::g_device_error), sizeof(int), 0,
+                              hipMemcpyDeviceToHost));
+  if (v) {
+    const int zero = 0;
+    MOE_HIP(hipMemcpyToSymbol(HIP_SYMBOL(moe::g_device_error), &zero, sizeof(int), 0,
+                              hipMemcpyHostToDevice));
+    return fail(MOE_ERR_DEVICE, "a kernel resolved an out-of-range slot reference");
+  }
+  return MOE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,111 @@
+// Device-side helpers shared by the gfx950 kernels of the expert hot path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/moe_stream.h"
+
+namespace moe {
+
+// Set by kernels when a slot reference is out of range for the pool view it
+// is resolved against; read and cleared by moe_check_device_error().
+extern __device__ int g_device_error;
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (weights are read once per launch).
+__device__ __forceinline__ uint4 load_stream16(const uint4 *p) {
+  u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// --- bf16 <-> f32 -----------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+// round to nearest even (inputs are finite here; NaN stays NaN)
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ float round_bf16(float f) {
+  return bf16_to_f32(f32_to_bf16(f));
+}
+
+// v_dot2c_f32_bf16: acc + a.lo*b.lo + a.hi*b.hi, fp32 accumulation.
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), acc,
+                                         false);
+}
+
+// Four packed bf16 pairs (128+q) from one word of eight 4-bit codes.  Pair m
+// holds codes m (low half) and m+4 (high half): 0x4300 is bf16 128.0 and its
+// 7-bit mantissa takes the code exactly, so no conversion instruction runs.
+__device__ __forceinline__ void codes_to_bf16x2(uint32_t w, uint32_t p[4]) {
+  const uint32_t M = 0x000f000fu, E = 0x43004300u;
+  p[0] = (w & M) | E;
+  p[1] = ((w >> 4) & M) | E;
+  p[2] = ((w >> 8) & M) | E;
+  p[3] = ((w >> 12) & M) | E;
+}
+
+// Eight consecutive bf16 activations (4 words) rearranged into the pair order
+// of codes_to_bf16x2: out[m] = (x[m], x[m+4]).
+__device__ __forceinline__ void x_pairs(const uint32_t in[4], uint32_t out[4]) {
+  out[0] = (in[0] & 0xffffu) | (in[2] << 16);
+  out[1] = (in[0] >> 16) | (in[2] & 0xffff0000u);
+  out[2] = (in[1] & 0xffffu) | (in[3] << 16);
+  out[3] = (in[1] >> 16) | (in[3] & 0xffff0000u);
+}
+
+// Sum over SG consecutive lanes (SG a power of two <= 64); every lane of the
+// group ends with the total.
+template <int SG>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = SG / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Pool view passed to kernels by value.
+struct PoolArgs {
+  const char *base[MOE_MAX_COMPONENTS];
+  int64_t slot_bytes[MOE_MAX_COMPONENTS];
+  const char *store;
+  int64_t record_bytes;
+  int64_t comp_offset[MOE_MAX_COMPONENTS];
+  int32_t n_slots;
+  int32_t n_records;
+};
+
+// Base address of component c for a slot reference; nullptr when the
+// reference is out of range (the caller then contributes nothing and the
+// device error word is set).
+__device__ __forceinline__ const char *resolve(const PoolArgs &pa, int c,
+                                               int32_t ref) {
+  if (ref >= 0) {
+    if (ref >= pa.n_slots) return nullptr;
+    return pa.base[c] + (int64_t)ref * pa.slot_bytes[c];
+  }
+  int64_t r = -(int64_t)ref - 1;
+  if (pa.store == nullptr || r >= pa.n_records) return nullptr;
+  return pa.store + r * pa.record_bytes + pa.comp_offset[c];
+}
+
+__device__ __forceinline__ void flag_error() {
+  __hip_atomic_store(&g_device_error, 1, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Component indices inside a pool view.
+__host__ __device__ constexpr int comp_index(int proj, int part, int nparts) {
+  return proj * nparts + part;
+}
+enum { PROJ_GATE = 0, PROJ_UP = 1, PROJ_DOWN = 2 };
+enum { PART_W = 0, PART_S = 1, PART_B = 2, PART_BIAS = 3 };
+
+}  // namespace moe

@@ -1,0 +1,56 @@
+// Host-side launchers of the gfx950 kernels, shared by the C ABI layer.
+#pragma once
+
+#include "common.h"
+
+namespace moe {
+
+// ---- batch-1 / small-T expert block (ffn_decode.hip) ----------------------
+struct FfnLaunch {
+  int d_model, d_ff, has_bias;
+  int up_rows_wg, up_threads;  // gate/up kernel: rows and threads per WG
+  int down_rows_wg;            // down kernel: output rows per WG
+  void (*up)(dim3, dim3, hipStream_t, const PoolArgs &, const int32_t *,
+             const uint16_t *, int, uint16_t *, int, float, float);
+  void (*down)(dim3, dim3, hipStream_t, const PoolArgs &, const int32_t *,
+               const float *, const uint16_t *, int, uint16_t *, float *);
+};
+const FfnLaunch *find_ffn(int d_model, int d_ff, int has_bias);
+void launch_ffn_up(const FfnLaunch *L, const PoolArgs &pa, const int32_t *refs,
+                   const uint16_t *x, int T, int k, uint16_t *h, int act,
+                   float alpha, float limit, hipStream_t s);
+void launch_ffn_down(const FfnLaunch *L, const PoolArgs &pa,
+                     const int32_t *refs, const float *scores, int T, int k,
+                     const uint16_t *h, uint16_t *out, float *out32,
+                     hipStream_t s);
+void launch_ffn_decode(const FfnLaunch *L, const PoolArgs &pa,
+                       const int32_t *refs, const float *scores,
+                       const uint16_t *x, int T, int k, uint16_t *h,
+                       uint16_t *out, float *out32, int act, float alpha,
+                       float limit, hipStream_t s);
+
+// ---- router / top-k / lookahead / slot lookup (route.hip) -----------------
+constexpr int kRouteMaxE = 128;
+constexpr int kRouteMaxT = 16;
+
+struct RouteArgs {
+  const uint16_t *x;
+  const uint16_t *W;
+  const uint16_t *bias;
+  const uint16_t *Wn;
+  const uint16_t *bias_n;
+  int32_t *ids;
+  float *scores;
+  int32_t *pred;
+  const int32_t *table;
+  int32_t *slot_refs;
+  int32_t *miss_count;
+  float *logits;      // [2][T][E] fp32 workspace
+  uint32_t *counter;  // workspace word, zero between launches
+  int T, D, E, mode, renorm, k, kp;
+};
+void launch_route(const RouteArgs &a, hipStream_t s);
+void launch_slot_lookup(const int32_t *table, int E, const int32_t *ids, int n,
+                        int32_t *refs, int32_t *miss_count, hipStream_t s);
+
+}  // namespace moe

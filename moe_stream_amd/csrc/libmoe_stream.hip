@@ -1,0 +1,5 @@
+// Single translation unit of the shared library (the kernels share one
+// device error word without relocatable device code).
+#include "ffn_decode.hip"
+#include "route.hip"
+#include "capi.hip"

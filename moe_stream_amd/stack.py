@@ -1,0 +1,134 @@
+"""Multi-layer bs=1 decode over an HBM-resident slot pool, routing on device.
+
+Per layer L of a token: one launch routes x_L through layer L's router
+(top-k, scores), runs layer L+1's router on the same x_L for the lookahead
+prediction (top_k_indices, engine_v3.py:509-515) and looks the routed experts
+up in the device slot table; then the two expert-block kernels read the
+routed slots.  No host round trip per layer: the reference's per-layer
+`mx.eval` + `np.array(inds)` + `acquire` (engine_v3.py:515-552) becomes a
+device-side table lookup, so a whole token can be captured as one HIP graph.
+
+Residency: a pool of n_slots holds the most popular (layer, expert) pairs;
+the slot table maps every pair either to its pool slot (ref >= 0) or, for a
+pair not in the pool, to its record in the HBM expert store (ref < 0), which
+the kernels read directly.  Both hold identical bytes, so outputs do not
+depend on residency (slot-permutation / pool-size invariance).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _lib, ops, synth
+from .geometry import Geometry
+from .pool import SlotPool
+
+
+class DecodeStack:
+    def __init__(self, geom: Geometry, n_layers: int, n_slots: int, device="cuda",
+                 seed: int = synth.SEED_BASE + 2, zipf_s: float | None = 1.1,
+                 router_bias: bool = False, widen: int = 1, resident=None):
+        self.geom = geom
+        self.L = n_layers
+        self.E = geom.n_experts
+        self.k = geom.top_k
+        self.device = torch.device(device)
+        self.widen = widen
+        self.k_pred = min(self.k * widen, self.E)
+        n_rec = n_layers * self.E
+        self.store = synth.make_store(geom, n_rec, self.device, seed)
+        self.pool = SlotPool(geom, n_slots, self.device, store=self.store)
+        W, b = synth.router_weights(geom, n_layers, self.device, seed + 1,
+                                    with_bias=router_bias)
+        self.W = W
+        self.logpop = None
+        if zipf_s is not None:
+            self.logpop = synth.zipf_log_popularity(n_layers, self.E, zipf_s, seed + 2)
+            zb = synth.bf16_bias_from_log(self.logpop, self.device)
+            b = zb if b is None else (b.float() + zb.float()).to(torch.bfloat16)
+        self.bias = b
+        # residency: `resident` (layer, expert) pairs in the pool, in a seeded
+        # random slot placement; the rest read from the store
+        if resident is None:
+            if self.logpop is not None:
+                resident = synth.popular_pairs(self.logpop, max(1, n_slots // n_layers))
+            else:
+                rng = np.random.default_rng(seed + 3)
+                per = max(1, n_slots // n_layers)
+                resident = [(Lx, int(e)) for Lx in range(n_layers)
+                            for e in np.sort(rng.permutation(self.E)[:per])]
+        resident = resident[:n_slots]
+        slots = synth.slot_permutation(n_slots, len(resident), seed + 4)
+        table = -(np.arange(n_rec, dtype=np.int64) + 1)
+        recs = np.array([Lx * self.E + e for Lx, e in resident], dtype=np.int64)
+        table[recs] = slots
+        self.table_host = table.reshape(n_layers, self.E).astype(np.int32)
+        self.table = torch.tensor(self.table_host, device=self.device)
+        self.pool.fill(recs, slots)
+        # per-layer device outputs
+        self.bufs = [ops.RouteBuffers(1, self.k, self.k_pred, self.device)
+                     for _ in range(n_layers)]
+        self.route_ws = torch.zeros(_lib.lib().moe_route_workspace(1, self.E),
+                                    dtype=torch.uint8, device=self.device)
+        g = geom.c_geom()
+        import ctypes as C
+        self.ffn_ws = torch.zeros(_lib.lib().moe_ffn_decode_workspace(C.byref(g), 1, self.k),
+                                  dtype=torch.uint8, device=self.device)
+        self.x_in = torch.zeros((n_layers, geom.d_model), dtype=torch.bfloat16,
+                                device=self.device)
+        self.y = torch.zeros((n_layers, geom.d_model), dtype=torch.bfloat16,
+                             device=self.device)
+        self.graph = None
+
+    # -- one token ----------------------------------------------------------
+    def layer(self, Lx: int, stream=None):
+        g = self.geom
+        nxt = Lx + 1 < self.L
+        b = self.bias[Lx] if self.bias is not None else None
+        bn = self.bias[Lx + 1] if (self.bias is not None and nxt) else None
+        bufs = self.bufs[Lx]
+        ops.route(self.x_in[Lx:Lx + 1], self.W[Lx], b, g.routing,
+                  g.norm_topk_prob, self.k,
+                  W_next=self.W[Lx + 1] if nxt else None, bias_next=bn,
+                  k_pred=self.k_pred, table=self.table[Lx], bufs=bufs,
+                  stream=stream, workspace=self.route_ws)
+        ops.ffn_decode(self.pool, bufs.slot_refs, bufs.scores,
+                       self.x_in[Lx:Lx + 1], out=self.y[Lx:Lx + 1],
+                       stream=stream, workspace=self.ffn_ws)
+
+    def token_eager(self, stream=None):
+        for Lx in range(self.L):
+            self.layer(Lx, stream)
+
+    def capture(self):
+        """Capture one token (all layers) as a HIP graph."""
+        s = torch.cuda.Stream(device=self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(s):
+            self.token_eager()          # warm the launch path outside capture
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        torch.cuda.synchronize(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.token_eager()
+        return self.graph
+
+    def run_token(self, x_tok: torch.Tensor, use_graph: bool = True):
+        """x_tok: bf16 [n_layers, d_model], the residual stream of one token."""
+        self.x_in.copy_(x_tok, non_blocking=True)
+        if use_graph and self.graph is not None:
+            self.graph.replay()
+        else:
+            self.token_eager()
+
+    # -- bookkeeping --------------------------------------------------------
+    def expert_bytes_per_token(self) -> int:
+        return self.L * self.k * self.geom.payload_bytes
+
+    def routed(self):
+        """Host copy of this token's routing: ids, scores, refs, preds."""
+        ids = torch.stack([b.ids[0] for b in self.bufs]).cpu().numpy()
+        sc = torch.stack([b.scores[0] for b in self.bufs]).cpu().numpy()
+        refs = torch.stack([b.slot_refs[0] for b in self.bufs]).cpu().numpy()
+        pred = torch.stack([b.pred[0] for b in self.bufs]).cpu().numpy()
+        return ids, sc, refs, pred
