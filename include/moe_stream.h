@@ -132,6 +132,8 @@ int moe_ffn_decode_down(const moe_pool_view *pool, const moe_geom *g,
  *   mode TOPK_SOFTMAX: top-k of logits; scores = bf16(softmax(selected))
  *     (top_k_route, engine_120b.py:65-70).
  * ids are ranked (value descending, ties to the lower expert id).
+ * Limits: T <= 16, E <= 128, d_model <= 4096 (multiple of 8), k <= 16,
+ *   k_pred <= 64.
  * Lookahead (W_next != NULL): pred_ids[t, 0..k_pred) = top-k_pred of the raw
  *   bf16 logits of x @ W_next.T (+ bias_next) (top_k_indices,
  *   engine_v3.py:476-483, engine_120b.py:73-75).
@@ -187,6 +189,45 @@ int moe_event_elapsed_ms(void *start, void *stop, float *ms);
 /* Read and clear the device error word set by the kernels (out-of-range slot
  * refs), synchronising `stream`.  Returns MOE_OK or MOE_ERR_DEVICE. */
 int moe_check_device_error(void *stream);
+
+/*
+ * Slot-pool bookkeeping (host only, no device calls): the (layer, expert) ->
+ * slot table with sampled LFU/LRU eviction of ExpertPool
+ * (engine_v3.py:213-236 state, :303-380 _alloc/_touch, :383-396 prefetch,
+ * :398-454 acquire, :456-464 stats).  Fills are the caller's job: prefetch
+ * and acquire report which slots to fill with which experts.  A prefetch
+ * stays pending until moe_policy_complete (the fill finished) or until an
+ * acquire of that expert waits on it.
+ */
+typedef struct moe_policy moe_policy;
+enum { MOE_EVICT_LFU = 0, MOE_EVICT_LRU = 1, MOE_EVICT_ASIS = 2 };
+
+/* window: entries younger than this many allocations are protected
+ * (24 * max(1, prefetch depth) in the reference). */
+int moe_policy_create(int32_t n_slots, int32_t n_layers, int32_t n_experts,
+                      int32_t evict, int32_t window, moe_policy **out);
+int moe_policy_destroy(moe_policy *p);
+/* Returns the number of fills issued (written to fill_slots/fill_experts,
+ * capacity n); *bailed = 1 when the pool was exhausted (silent bail). */
+int moe_policy_prefetch(moe_policy *p, int32_t layer, const int32_t *experts,
+                        int32_t n, int32_t *fill_slots, int32_t *fill_experts,
+                        int32_t *bailed);
+/* slots_out[i] = slot of experts[i]; miss_idx[0..*n_miss) = positions the
+ * caller must fill now; wait_idx[0..*n_wait) = positions whose prefetch fill
+ * the caller must wait for.  MOE_ERR_EXHAUSTED when every slot is pinned or
+ * pending. */
+int moe_policy_acquire(moe_policy *p, int32_t layer, const int32_t *experts,
+                       int32_t n, int32_t *slots_out, int32_t *miss_idx,
+                       int32_t *n_miss, int32_t *wait_idx, int32_t *n_wait);
+int moe_policy_complete(moe_policy *p, int32_t layer, int32_t expert);
+/* slot of (layer, expert) or -1 */
+int moe_policy_lookup(const moe_policy *p, int32_t layer, int32_t expert);
+int moe_policy_is_pending(const moe_policy *p, int32_t layer, int32_t expert);
+/* table[layer * n_experts + expert] = slot or -1 (the device slot table) */
+int moe_policy_table(const moe_policy *p, int32_t *table);
+/* out[8] = total, prefetch hits, cache hits, misses, prefetch bails,
+ * prefetches issued, allocation clock, use clock */
+int moe_policy_stats(const moe_policy *p, int64_t *out);
 
 #ifdef __cplusplus
 }

@@ -37,7 +37,14 @@ EXPORTS = (
     "moe_event_create", "moe_event_destroy", "moe_event_record",
     "moe_event_query", "moe_stream_wait_event", "moe_event_elapsed_ms",
     "moe_check_device_error",
+    "moe_policy_create", "moe_policy_destroy", "moe_policy_prefetch",
+    "moe_policy_acquire", "moe_policy_complete", "moe_policy_lookup",
+    "moe_policy_is_pending", "moe_policy_table", "moe_policy_stats",
 )
+
+MOE_EVICT_LFU = 0
+MOE_EVICT_LRU = 1
+MOE_EVICT_ASIS = 2
 
 
 class MoeError(RuntimeError):
@@ -92,6 +99,15 @@ def _declare(lib):
         "moe_stream_wait_event": (C.c_int, [P, P]),
         "moe_event_elapsed_ms": (C.c_int, [P, P, C.POINTER(F)]),
         "moe_check_device_error": (C.c_int, [P]),
+        "moe_policy_create": (C.c_int, [I32, I32, I32, I32, I32, C.POINTER(C.c_void_p)]),
+        "moe_policy_destroy": (C.c_int, [P]),
+        "moe_policy_prefetch": (C.c_int, [P, I32, P, I32, P, P, P]),
+        "moe_policy_acquire": (C.c_int, [P, I32, P, I32, P, P, P, P, P]),
+        "moe_policy_complete": (C.c_int, [P, I32, I32]),
+        "moe_policy_lookup": (C.c_int, [P, I32, I32]),
+        "moe_policy_is_pending": (C.c_int, [P, I32, I32]),
+        "moe_policy_table": (C.c_int, [P, P]),
+        "moe_policy_stats": (C.c_int, [P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

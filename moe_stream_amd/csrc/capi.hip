@@ -147,6 +147,9 @@ static int ffn_prepare(const moe_pool_view *pool, const moe_geom *g,
     return fail(MOE_ERR_UNSUPPORTED,
                 "no decode kernel compiled for d_model=%d d_ff=%d proj_bias=%d",
                 g->d_model, g->d_ff, g->has_proj_bias);
+  if ((*L)->down_lds(k) > 65536)
+    return fail(MOE_ERR_UNSUPPORTED, "k=%d needs %zu bytes of LDS in the down kernel (max 65536)",
+                k, (*L)->down_lds(k));
   return MOE_OK;
 }
 
@@ -223,8 +226,8 @@ int moe_route(const uint16_t *x, int32_t T, int32_t d_model, const uint16_t *W,
     return fail(MOE_ERR_INVALID, "T=%d outside [1, %d]", T, moe::kRouteMaxT);
   if (E <= 0 || E > moe::kRouteMaxE)
     return fail(MOE_ERR_INVALID, "E=%d outside [1, %d]", E, moe::kRouteMaxE);
-  if (d_model <= 0 || d_model % 8)
-    return fail(MOE_ERR_INVALID, "d_model=%d must be a positive multiple of 8", d_model);
+  if (d_model <= 0 || d_model % 8 || d_model > 4096)
+    return fail(MOE_ERR_INVALID, "d_model=%d must be a multiple of 8 in [8, 4096]", d_model);
   if (k <= 0 || k > MOE_MAX_TOPK || k > E)
     return fail(MOE_ERR_INVALID, "k=%d outside [1, min(E, %d)]", k, MOE_MAX_TOPK);
   if (mode != MOE_ROUTE_SOFTMAX_TOPK && mode != MOE_ROUTE_TOPK_SOFTMAX)
@@ -235,8 +238,8 @@ int moe_route(const uint16_t *x, int32_t T, int32_t d_model, const uint16_t *W,
     return fail(MOE_ERR_INVALID, "x and W must be 16-byte aligned");
   if (W_next) {
     if (!pred_ids) return fail(MOE_ERR_INVALID, "W_next given without pred_ids");
-    if (k_pred <= 0 || k_pred > E)
-      return fail(MOE_ERR_INVALID, "k_pred=%d outside [1, E]", k_pred);
+    if (k_pred <= 0 || k_pred > E || k_pred > 64)
+      return fail(MOE_ERR_INVALID, "k_pred=%d outside [1, min(E, 64)]", k_pred);
     if (!aligned(W_next, 16)) return fail(MOE_ERR_INVALID, "W_next misaligned");
   }
   if (table && !slot_refs) return fail(MOE_ERR_INVALID, "table given without slot_refs");

@@ -42,15 +42,42 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
                                          false);
 }
 
+// (w & M) | E in one v_bfi_b32 (E has no bits inside M).
+__device__ __forceinline__ uint32_t bfi_mask(uint32_t w, uint32_t M, uint32_t E) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(M), "v"(w), "v"(E));
+  return r;
+}
+
 // Four packed bf16 pairs (128+q) from one word of eight 4-bit codes.  Pair m
 // holds codes m (low half) and m+4 (high half): 0x4300 is bf16 128.0 and its
 // 7-bit mantissa takes the code exactly, so no conversion instruction runs.
 __device__ __forceinline__ void codes_to_bf16x2(uint32_t w, uint32_t p[4]) {
   const uint32_t M = 0x000f000fu, E = 0x43004300u;
-  p[0] = (w & M) | E;
-  p[1] = ((w >> 4) & M) | E;
-  p[2] = ((w >> 8) & M) | E;
-  p[3] = ((w >> 12) & M) | E;
+  p[0] = bfi_mask(w, M, E);
+  p[1] = bfi_mask(w >> 4, M, E);
+  p[2] = bfi_mask(w >> 8, M, E);
+  p[3] = bfi_mask(w >> 12, M, E);
+}
+
+// --- cross-lane reductions on DPP (no LDS round trip) -----------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+constexpr int kDppQuadXor1 = 0xb1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4e;      // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;   // row_half_mirror
+constexpr int kDppMirror = 0x140;       // row_mirror
+constexpr int kSwizzleXor16 = 0x401f;   // ds_swizzle bitmask mode, xor 16
+
+__device__ __forceinline__ float swz_xor16_f(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), kSwizzleXor16));
 }
 
 // Eight consecutive bf16 activations (4 words) rearranged into the pair order
@@ -63,12 +90,30 @@ __device__ __forceinline__ void x_pairs(const uint32_t in[4], uint32_t out[4]) {
 }
 
 // Sum over SG consecutive lanes (SG a power of two <= 64); every lane of the
-// group ends with the total.
+// group ends with the total (each pairwise sum is commutative, so all lanes
+// hold the identical value).  Quad and mirror DPP steps inside a 16-lane row,
+// a swizzle across rows of 32, readlanes across halves of 64.
 template <int SG>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int off = SG / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  if (SG >= 2) v += dpp_f<kDppQuadXor1>(v);
+  if (SG >= 4) v += dpp_f<kDppQuadXor2>(v);
+  if (SG >= 8) v += dpp_f<kDppHalfMirror>(v);
+  if (SG >= 16) v += dpp_f<kDppMirror>(v);
+  if (SG >= 32) v += swz_xor16_f(v);
+  if (SG >= 64)
+    v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
   return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f<kDppMirror>(v));
+  v = fmaxf(v, swz_xor16_f(v));
+  return fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)),
+               __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)));
 }
 
 // Pool view passed to kernels by value.

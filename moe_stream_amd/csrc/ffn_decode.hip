@@ -18,55 +18,49 @@
 //
 // Work mapping: SG lanes share one weight row; lane j of a row reads 16-byte
 // chunks j, j+SG, j+2SG, ... so each load instruction of a wave covers
-// 64/SG rows with SG*16 contiguous bytes each.  A lane always sees the same
-// input chunks, so the activations it needs sit in registers, already in
-// the pair order of the decoded codes, for the whole kernel.  Row sums are an
-// SG-lane butterfly.  All code loads of a lane are issued before any math.
+// 64/SG rows with SG*16 contiguous bytes each.  Every lane issues all of its
+// code loads first; while they are in flight the workgroup stages the
+// activations (already rearranged into the pair order of the decoded codes,
+// with per-chunk sums) and the rows' scales and biases in LDS with coalesced
+// 16-byte loads.  Row sums are an SG-lane butterfly.
 #include "launchers.h"
 
 namespace moe {
 
 __device__ int g_device_error = 0;
 
-template <int CPL, int SG, int U>
-__device__ __forceinline__ void load_act_chunks(const uint16_t *__restrict__ v,
-                                                int j, uint32_t (&xp)[CPL][16],
-                                                float (&xs)[CPL]) {
-  const uint4 *v4 = reinterpret_cast<const uint4 *>(v);
+// Stage one 16-byte piece (8 activations, index i of the row) into LDS in
+// pair order: act[q*U + c] holds pieces q=0..3 of chunk c, so the lanes of a
+// row, which read consecutive chunks, hit consecutive 16-byte LDS slots.
+// Returns the 8-value partial sum; the caller reduces it over the 4 pieces
+// of a chunk (4 consecutive lanes).
+template <int U>
+__device__ __forceinline__ float stage_piece(uint4 *act, int i, uint4 a) {
+  const int c = i >> 2, q = i & 3;
+  uint32_t in[4] = {a.x, a.y, a.z, a.w}, out[4];
+  x_pairs(in, out);
+  act[q * U + c] = make_uint4(out[0], out[1], out[2], out[3]);
+  float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < CPL; ++i) {
-    const int c = i * SG + j;
-    xs[i] = 0.f;
-    if (CPL * SG == U || c < U) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {  // 8 activations per uint4
-        uint4 a = v4[c * 4 + q];
-        uint32_t in[4] = {a.x, a.y, a.z, a.w};
-        uint32_t out[4];
-        x_pairs(in, out);
-#pragma unroll
-        for (int m = 0; m < 4; ++m) xp[i][q * 4 + m] = out[m];
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-          xs[i] += bf16_to_f32(in[m] & 0xffffu) + bf16_to_f32(in[m] >> 16);
-      }
-    } else {
-#pragma unroll
-      for (int m = 0; m < 16; ++m) xp[i][m] = 0u;
-    }
-  }
+  for (int m = 0; m < 4; ++m) s += bf16_to_f32(in[m] & 0xffffu) + bf16_to_f32(in[m] >> 16);
+  return s;
 }
 
-// sum((128+q)*x) over one 16-byte chunk of codes (32 inputs).
-__device__ __forceinline__ float chunk_dot(const uint4 &c, const uint32_t *xp) {
+// sum((128+q)*x) over one 16-byte chunk of codes (32 inputs), activations
+// from LDS in pair order.
+template <int U>
+__device__ __forceinline__ float chunk_dot_lds(const uint4 &c, const uint4 *act,
+                                               int chunk) {
   float acc = 0.f;
   const uint32_t w[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
+    const uint4 xa = act[q * U + chunk];
+    const uint32_t xv[4] = {xa.x, xa.y, xa.z, xa.w};
     uint32_t p[4];
     codes_to_bf16x2(w[q], p);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) acc = dot2_bf16(p[m], xp[q * 4 + m], acc);
+    for (int m = 0; m < 4; ++m) acc = dot2_bf16(p[m], xv[m], acc);
   }
   return acc;
 }
@@ -97,36 +91,65 @@ __global__ __launch_bounds__(WAVES * 64) void ffn_gate_up_kernel(
   constexpr int WG_PER_PAIR = F / ROWS_WG;
   constexpr int NG = D / 64;                // quant groups per row
   constexpr int NP = PBIAS ? 4 : 3;
+  constexpr int NT = WAVES * 64;
+  constexpr int XU4 = D / 8;                // 16-byte pieces of x
+  constexpr int SB_U4 = ROWS_WG * NG * 2 / 16;  // 16-byte pieces per scale block
   static_assert(F % ROWS_WG == 0, "rows per workgroup must divide d_ff");
+  static_assert((ROWS_WG * NG * 2) % 16 == 0, "scale block must be 16-byte pieces");
+
+  __shared__ uint4 act_l[4 * U];
+  __shared__ float asum_l[U];
+  __shared__ uint4 sb_l[4][SB_U4];          // gate S, gate B, up S, up B
 
   const int pair = blockIdx.x / WG_PER_PAIR;
   const int rb = blockIdx.x % WG_PER_PAIR;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int rsub = lane / SG, j = lane % SG;
   const int t = pair / k;
   const int32_t ref = refs[pair];
+  const int row0 = rb * ROWS_WG;
 
   const char *gw = resolve(pa, comp_index(PROJ_GATE, PART_W, NP), ref);
-  const char *uw = resolve(pa, comp_index(PROJ_UP, PART_W, NP), ref);
-  const char *gsc = resolve(pa, comp_index(PROJ_GATE, PART_S, NP), ref);
-  const char *usc = resolve(pa, comp_index(PROJ_UP, PART_S, NP), ref);
-  const char *gbi = resolve(pa, comp_index(PROJ_GATE, PART_B, NP), ref);
-  const char *ubi = resolve(pa, comp_index(PROJ_UP, PART_B, NP), ref);
   if (gw == nullptr) {  // uniform over the workgroup
-    if (threadIdx.x == 0) flag_error();
-#pragma unroll
-    for (int s = 0; s < RSTEPS; ++s) {
-      const int row = rb * ROWS_WG + (wave * RSTEPS + s) * RPS + rsub;
-      if (j == 0) h[(int64_t)pair * F + row] = 0;
-    }
+    if (tid == 0) flag_error();
+    for (int r = tid; r < ROWS_WG; r += NT) h[(int64_t)pair * F + row0 + r] = 0;
     return;
   }
+  const char *uw = resolve(pa, comp_index(PROJ_UP, PART_W, NP), ref);
 
-  // 1. issue every code load of this lane
+  // 1. the small loads first (activations, scales/biases: 16 bytes per
+  //    thread), so that staging them into LDS only waits for them and not
+  //    for the code stream issued after them (loads retire in order)
+  constexpr int XIT = (XU4 + NT - 1) / NT;
+  constexpr int SIT = (4 * SB_U4 + NT - 1) / NT;
+  uint4 xr[XIT], sr[SIT];
+  {
+    const uint4 *x4 = reinterpret_cast<const uint4 *>(x + (int64_t)t * D);
+#pragma unroll
+    for (int it = 0; it < XIT; ++it) {
+      const int i = it * NT + tid;
+      xr[it] = (i < XU4) ? x4[i] : make_uint4(0, 0, 0, 0);
+    }
+    const char *sbp[4] = {resolve(pa, comp_index(PROJ_GATE, PART_S, NP), ref),
+                          resolve(pa, comp_index(PROJ_GATE, PART_B, NP), ref),
+                          resolve(pa, comp_index(PROJ_UP, PART_S, NP), ref),
+                          resolve(pa, comp_index(PROJ_UP, PART_B, NP), ref)};
+#pragma unroll
+    for (int it = 0; it < SIT; ++it) {
+      const int i = it * NT + tid;
+      const int p = i / SB_U4, o = i % SB_U4;
+      sr[it] = (i < 4 * SB_U4)
+                   ? reinterpret_cast<const uint4 *>(sbp[p] + (int64_t)row0 * NG * 2)[o]
+                   : make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  // 2. every code load of this lane
   uint4 cg[RSTEPS][CPL], cu[RSTEPS][CPL];
 #pragma unroll
   for (int s = 0; s < RSTEPS; ++s) {
-    const int row = rb * ROWS_WG + (wave * RSTEPS + s) * RPS + rsub;
+    const int row = row0 + (wave * RSTEPS + s) * RPS + rsub;
     const uint4 *g4 = reinterpret_cast<const uint4 *>(gw + (int64_t)row * (D / 2));
     const uint4 *u4 = reinterpret_cast<const uint4 *>(uw + (int64_t)row * (D / 2));
 #pragma unroll
@@ -141,48 +164,46 @@ __global__ __launch_bounds__(WAVES * 64) void ffn_gate_up_kernel(
       }
     }
   }
-  // 2. scales and biases of the groups this lane touches
-  uint16_t sg_[RSTEPS][CPL], bg_[RSTEPS][CPL], su_[RSTEPS][CPL], bu_[RSTEPS][CPL];
+  // 3. stage scales/biases and the activations (pair order + chunk sums)
 #pragma unroll
-  for (int s = 0; s < RSTEPS; ++s) {
-    const int row = rb * ROWS_WG + (wave * RSTEPS + s) * RPS + rsub;
-    const uint16_t *gS = reinterpret_cast<const uint16_t *>(gsc) + row * NG;
-    const uint16_t *uS = reinterpret_cast<const uint16_t *>(usc) + row * NG;
-    const uint16_t *gB = reinterpret_cast<const uint16_t *>(gbi) + row * NG;
-    const uint16_t *uB = reinterpret_cast<const uint16_t *>(ubi) + row * NG;
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int c = i * SG + j;
-      const int g = (CPL * SG == U || c < U) ? c / 2 : 0;
-      sg_[s][i] = gS[g];
-      bg_[s][i] = gB[g];
-      su_[s][i] = uS[g];
-      bu_[s][i] = uB[g];
-    }
+  for (int it = 0; it < SIT; ++it) {
+    const int i = it * NT + tid;
+    if (i < 4 * SB_U4) (&sb_l[0][0])[i] = sr[it];
   }
-  // 3. activations of this token, in registers
-  uint32_t xp[CPL][16];
-  float xs[CPL];
-  load_act_chunks<CPL, SG, U>(x + (int64_t)t * D, j, xp, xs);
+#pragma unroll
+  for (int it = 0; it < XIT; ++it) {
+    const int i = it * NT + tid;
+    float s = 0.f;
+    if (i < XU4) s = stage_piece<U>(act_l, i, xr[it]);
+    s += dpp_f<kDppQuadXor1>(s);   // the 4 pieces of a chunk: 4 adjacent lanes
+    s += dpp_f<kDppQuadXor2>(s);
+    if (i < XU4 && (i & 3) == 0) asum_l[i >> 2] = s;
+  }
+  __syncthreads();
 
+  const uint16_t *sbh = reinterpret_cast<const uint16_t *>(&sb_l[0][0]);
+  constexpr int SBN = SB_U4 * 8;  // bf16 per scale block
   // 4. dot products, row sums, activation
 #pragma unroll
   for (int s = 0; s < RSTEPS; ++s) {
+    const int rl = (wave * RSTEPS + s) * RPS + rsub;  // row inside the WG
     float pg = 0.f, pu = 0.f;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
       const int c = i * SG + j;
       if (CPL * SG == U || c < U) {
-        const float Sg = bf16_to_f32(sg_[s][i]), Bg = bf16_to_f32(bg_[s][i]);
-        const float Su = bf16_to_f32(su_[s][i]), Bu = bf16_to_f32(bu_[s][i]);
-        pg += Sg * chunk_dot(cg[s][i], xp[i]) + (Bg - 128.f * Sg) * xs[i];
-        pu += Su * chunk_dot(cu[s][i], xp[i]) + (Bu - 128.f * Su) * xs[i];
+        const int g = rl * NG + (c >> 1);
+        const float Sg = bf16_to_f32(sbh[0 * SBN + g]), Bg = bf16_to_f32(sbh[1 * SBN + g]);
+        const float Su = bf16_to_f32(sbh[2 * SBN + g]), Bu = bf16_to_f32(sbh[3 * SBN + g]);
+        const float xs = asum_l[c];
+        pg += Sg * chunk_dot_lds<U>(cg[s][i], act_l, c) + (Bg - 128.f * Sg) * xs;
+        pu += Su * chunk_dot_lds<U>(cu[s][i], act_l, c) + (Bu - 128.f * Su) * xs;
       }
     }
     pg = group_sum<SG>(pg);
     pu = group_sum<SG>(pu);
     if (j == 0) {
-      const int row = rb * ROWS_WG + (wave * RSTEPS + s) * RPS + rsub;
+      const int row = row0 + rl;
       if (PBIAS) {
         const uint16_t *gbias = reinterpret_cast<const uint16_t *>(
             resolve(pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref));
@@ -197,24 +218,45 @@ __global__ __launch_bounds__(WAVES * 64) void ffn_gate_up_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// down + weighted combine; one wave per routed expert, blockDim = 64*k
+// down + weighted combine; one wave per routed expert, blockDim = 64*k.
+// Dynamic LDS per wave: h in pair order (4*U pieces), chunk sums (U floats),
+// scales and biases of the workgroup's rows; then the combine buffer.
 // ---------------------------------------------------------------------------
+template <int D, int F, int SG, int RSTEPS>
+struct DownLds {
+  static constexpr int U = F / 32;
+  static constexpr int RPS = 64 / SG;
+  static constexpr int ROWS_WG = RSTEPS * RPS;
+  static constexpr int NG = F / 64;
+  static constexpr int SB_U4 = ROWS_WG * NG * 2 / 16;
+  static constexpr int ACT_BYTES = 4 * U * 16;
+  static constexpr int SUM_BYTES = ((U * 4 + 15) / 16) * 16;
+  static constexpr int SB_BYTES = 2 * SB_U4 * 16;
+  static constexpr int WAVE_BYTES = ACT_BYTES + SUM_BYTES + SB_BYTES;
+  static constexpr size_t bytes(int k) {
+    return (size_t)k * WAVE_BYTES + (size_t)MOE_MAX_TOPK * ROWS_WG * 4;
+  }
+};
+
 template <int D, int F, int SG, int RSTEPS, bool PBIAS>
 __global__ __launch_bounds__(64 * MOE_MAX_TOPK) void ffn_down_kernel(
     PoolArgs pa, const int32_t *__restrict__ refs,
     const float *__restrict__ scores, const uint16_t *__restrict__ h, int k,
     uint16_t *__restrict__ out, float *__restrict__ out32) {
-  constexpr int U = F / 32;
+  using LY = DownLds<D, F, SG, RSTEPS>;
+  constexpr int U = LY::U;
   constexpr int CPL = (U + SG - 1) / SG;
-  constexpr int RPS = 64 / SG;
-  constexpr int ROWS_WG = RSTEPS * RPS;
+  constexpr int RPS = LY::RPS;
+  constexpr int ROWS_WG = LY::ROWS_WG;
   constexpr int WG_PER_TOK = D / ROWS_WG;
-  constexpr int NG = F / 64;
+  constexpr int NG = LY::NG;
   constexpr int NP = PBIAS ? 4 : 3;
+  constexpr int SB_U4 = LY::SB_U4;
+  constexpr int HU4 = F / 8;
   static_assert(D % ROWS_WG == 0, "rows per workgroup must divide d_model");
+  static_assert((ROWS_WG * NG * 2) % 16 == 0, "scale block must be 16-byte pieces");
 
-  __shared__ float red[MOE_MAX_TOPK][ROWS_WG];
-
+  extern __shared__ uint4 dyn_lds[];
   const int t = blockIdx.x / WG_PER_TOK;
   const int rb = blockIdx.x % WG_PER_TOK;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -222,71 +264,102 @@ __global__ __launch_bounds__(64 * MOE_MAX_TOPK) void ffn_down_kernel(
   const int pair = t * k + wave;
   const int32_t ref = refs[pair];
   const float score = scores[pair];
+  const int row0 = rb * ROWS_WG;
+
+  char *wbase = reinterpret_cast<char *>(dyn_lds) + (size_t)wave * LY::WAVE_BYTES;
+  uint4 *act_l = reinterpret_cast<uint4 *>(wbase);
+  float *asum_l = reinterpret_cast<float *>(wbase + LY::ACT_BYTES);
+  uint4 *sb_l = reinterpret_cast<uint4 *>(wbase + LY::ACT_BYTES + LY::SUM_BYTES);
+  float *red = reinterpret_cast<float *>(reinterpret_cast<char *>(dyn_lds) +
+                                         (size_t)k * LY::WAVE_BYTES);
 
   const char *dw = resolve(pa, comp_index(PROJ_DOWN, PART_W, NP), ref);
+  uint4 cd[RSTEPS][CPL];
   if (dw != nullptr) {
-    const char *dsc = resolve(pa, comp_index(PROJ_DOWN, PART_S, NP), ref);
-    const char *dbi = resolve(pa, comp_index(PROJ_DOWN, PART_B, NP), ref);
-    uint4 cd[RSTEPS][CPL];
-    uint16_t sd[RSTEPS][CPL], bd[RSTEPS][CPL];
+    // small loads first (h of this expert, the rows' scales/biases), then
+    // the code stream; staging waits only for the former
+    constexpr int HIT = (HU4 + 63) / 64;
+    constexpr int SIT = (2 * SB_U4 + 63) / 64;
+    uint4 hr[HIT], sr[SIT];
+    const uint4 *h4 = reinterpret_cast<const uint4 *>(h + (int64_t)pair * F);
+#pragma unroll
+    for (int it = 0; it < HIT; ++it) {
+      const int i = it * 64 + lane;
+      hr[it] = (i < HU4) ? h4[i] : make_uint4(0, 0, 0, 0);
+    }
+    const char *sp = resolve(pa, comp_index(PROJ_DOWN, PART_S, NP), ref);
+    const char *bp = resolve(pa, comp_index(PROJ_DOWN, PART_B, NP), ref);
+#pragma unroll
+    for (int it = 0; it < SIT; ++it) {
+      const int i = it * 64 + lane;
+      const int p = i / SB_U4, o = i % SB_U4;
+      sr[it] = (i < 2 * SB_U4)
+                   ? reinterpret_cast<const uint4 *>((p ? bp : sp) + (int64_t)row0 * NG * 2)[o]
+                   : make_uint4(0, 0, 0, 0);
+    }
 #pragma unroll
     for (int s = 0; s < RSTEPS; ++s) {
-      const int row = rb * ROWS_WG + s * RPS + rsub;
+      const int row = row0 + s * RPS + rsub;
       const uint4 *d4 = reinterpret_cast<const uint4 *>(dw + (int64_t)row * (F / 2));
 #pragma unroll
       for (int i = 0; i < CPL; ++i) {
         const int c = i * SG + j;
-        cd[s][i] = (CPL * SG == U || c < U) ? load_stream16(d4 + c)
-                                            : make_uint4(0, 0, 0, 0);
+        cd[s][i] = (CPL * SG == U || c < U) ? load_stream16(d4 + c) : make_uint4(0, 0, 0, 0);
       }
     }
 #pragma unroll
-    for (int s = 0; s < RSTEPS; ++s) {
-      const int row = rb * ROWS_WG + s * RPS + rsub;
-      const uint16_t *S = reinterpret_cast<const uint16_t *>(dsc) + row * NG;
-      const uint16_t *B = reinterpret_cast<const uint16_t *>(dbi) + row * NG;
-#pragma unroll
-      for (int i = 0; i < CPL; ++i) {
-        const int c = i * SG + j;
-        const int g = (CPL * SG == U || c < U) ? c / 2 : 0;
-        sd[s][i] = S[g];
-        bd[s][i] = B[g];
-      }
+    for (int it = 0; it < SIT; ++it) {
+      const int i = it * 64 + lane;
+      if (i < 2 * SB_U4) sb_l[i] = sr[it];
     }
-    uint32_t hp[CPL][16];
-    float hs[CPL];
-    load_act_chunks<CPL, SG, U>(h + (int64_t)pair * F, j, hp, hs);
+#pragma unroll
+    for (int it = 0; it < HIT; ++it) {
+      const int i = it * 64 + lane;
+      float s = 0.f;
+      if (i < HU4) s = stage_piece<U>(act_l, i, hr[it]);
+      s += dpp_f<kDppQuadXor1>(s);
+      s += dpp_f<kDppQuadXor2>(s);
+      if (i < HU4 && (i & 3) == 0) asum_l[i >> 2] = s;
+    }
+  } else if (lane == 0) {
+    flag_error();
+  }
+  __syncthreads();
+
+  if (dw != nullptr) {
+    const uint16_t *sbh = reinterpret_cast<const uint16_t *>(sb_l);
+    constexpr int SBN = SB_U4 * 8;
 #pragma unroll
     for (int s = 0; s < RSTEPS; ++s) {
+      const int rl = s * RPS + rsub;
       float p = 0.f;
 #pragma unroll
       for (int i = 0; i < CPL; ++i) {
         const int c = i * SG + j;
         if (CPL * SG == U || c < U) {
-          const float Sd = bf16_to_f32(sd[s][i]), Bd = bf16_to_f32(bd[s][i]);
-          p += Sd * chunk_dot(cd[s][i], hp[i]) + (Bd - 128.f * Sd) * hs[i];
+          const int g = rl * NG + (c >> 1);
+          const float Sd = bf16_to_f32(sbh[g]), Bd = bf16_to_f32(sbh[SBN + g]);
+          p += Sd * chunk_dot_lds<U>(cd[s][i], act_l, c) + (Bd - 128.f * Sd) * asum_l[c];
         }
       }
       p = group_sum<SG>(p);
       if (j == 0) {
-        const int row = rb * ROWS_WG + s * RPS + rsub;
         if (PBIAS) {
           const uint16_t *dbias = reinterpret_cast<const uint16_t *>(
               resolve(pa, comp_index(PROJ_DOWN, PART_BIAS, NP), ref));
-          p += bf16_to_f32(dbias[row]);
+          p += bf16_to_f32(dbias[row0 + rl]);
         }
-        red[wave][s * RPS + rsub] = score * p;
+        red[wave * ROWS_WG + rl] = score * p;
       }
     }
   } else {
-    if (lane == 0) flag_error();
-    for (int i = lane; i < ROWS_WG; i += 64) red[wave][i] = 0.f;
+    for (int i = lane; i < ROWS_WG; i += 64) red[wave * ROWS_WG + i] = 0.f;
   }
   __syncthreads();
   for (int r = threadIdx.x; r < ROWS_WG; r += blockDim.x) {
     float y = 0.f;
-    for (int w = 0; w < k; ++w) y += red[w][r];  // expert order: deterministic
-    const int64_t o = (int64_t)t * D + rb * ROWS_WG + r;
+    for (int w = 0; w < k; ++w) y += red[w * ROWS_WG + r];  // expert order
+    const int64_t o = (int64_t)t * D + row0 + r;
     if (out) out[o] = (uint16_t)f32_to_bf16(y);
     if (out32) out32[o] = y;
   }
@@ -295,7 +368,6 @@ __global__ __launch_bounds__(64 * MOE_MAX_TOPK) void ffn_down_kernel(
 // ---------------------------------------------------------------------------
 // host-side dispatch over the compiled geometries
 // ---------------------------------------------------------------------------
-
 template <int D, int F, int SG, int WAVES, int RSTEPS, bool PBIAS>
 static void launch_up(dim3 g, dim3 b, hipStream_t s, const PoolArgs &pa,
                       const int32_t *refs, const uint16_t *x, int k,
@@ -307,18 +379,26 @@ template <int D, int F, int SG, int RSTEPS, bool PBIAS>
 static void launch_down(dim3 g, dim3 b, hipStream_t s, const PoolArgs &pa,
                         const int32_t *refs, const float *sc, const uint16_t *h,
                         int k, uint16_t *out, float *out32) {
-  hipLaunchKernelGGL((ffn_down_kernel<D, F, SG, RSTEPS, PBIAS>), g, b, 0, s, pa,
-                     refs, sc, h, k, out, out32);
+  const size_t lds = DownLds<D, F, SG, RSTEPS>::bytes(k);
+  hipLaunchKernelGGL((ffn_down_kernel<D, F, SG, RSTEPS, PBIAS>), g, b, lds, s,
+                     pa, refs, sc, h, k, out, out32);
+}
+
+template <int D, int F, int SG, int RSTEPS>
+static size_t down_lds_bytes(int k) {
+  return DownLds<D, F, SG, RSTEPS>::bytes(k);
 }
 
 #define MOE_FFN_GEOM(D, F, PB, SGU, WU, RU, SGD, RD)                         \
   {D, F, PB, (WU) * (RU) * (64 / (SGU)), (WU) * 64, (RD) * (64 / (SGD)),     \
-   &launch_up<D, F, SGU, WU, RU, PB>, &launch_down<D, F, SGD, RD, PB>}
+   &launch_up<D, F, SGU, WU, RU, PB>, &launch_down<D, F, SGD, RD, PB>,       \
+   &down_lds_bytes<D, F, SGD, RD>}
 
 // d_model, d_ff, proj bias | gate/up: SG, waves, row steps | down: SG, steps
 static const FfnLaunch kFfnTable[] = {
-    MOE_FFN_GEOM(2048, 768, false, 16, 4, 1, 8, 1),   // Qwen3-30B-A3B
-    MOE_FFN_GEOM(2048, 768, true, 16, 4, 1, 8, 1),
+    // Qwen3-30B-A3B: 24 rows per workgroup -> 8 experts x 32 = 256 WGs
+    MOE_FFN_GEOM(2048, 768, false, 16, 6, 1, 8, 1),
+    MOE_FFN_GEOM(2048, 768, true, 16, 6, 1, 8, 1),
     MOE_FFN_GEOM(2880, 2880, true, 32, 4, 2, 32, 4),  // gpt-oss-120b
     MOE_FFN_GEOM(2880, 2880, false, 32, 4, 2, 32, 4),
     MOE_FFN_GEOM(256, 128, false, 8, 2, 1, 4, 1),     // small test geometry

@@ -14,6 +14,7 @@ struct FfnLaunch {
              const uint16_t *, int, uint16_t *, int, float, float);
   void (*down)(dim3, dim3, hipStream_t, const PoolArgs &, const int32_t *,
                const float *, const uint16_t *, int, uint16_t *, float *);
+  size_t (*down_lds)(int k);   // dynamic LDS bytes of the down kernel
 };
 const FfnLaunch *find_ffn(int d_model, int d_ff, int has_bias);
 void launch_ffn_up(const FfnLaunch *L, const PoolArgs &pa, const int32_t *refs,

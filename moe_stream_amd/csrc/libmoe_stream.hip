@@ -3,3 +3,4 @@
 #include "ffn_decode.hip"
 #include "route.hip"
 #include "capi.hip"
+#include "policy.cpp"

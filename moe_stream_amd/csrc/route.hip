@@ -1,13 +1,17 @@
 // Router, top-k, lookahead and slot lookup for a few tokens, one launch.
 //
 // Phase 1 (every workgroup): one wave per router row computes the fp32 dot
-// x_t . W[e] for each token (bf16 pairs through v_dot2c_f32_bf16) and stores
-// it to the workspace.  Rows 0..E-1 are this layer's router, rows E..2E-1 the
-// next layer's router (lookahead), when present.
-// Phase 2 (the last workgroup to finish, found with an acq_rel counter):
-// bf16 logits, softmax / ranking, scores, lookahead ids and the slot-table
-// lookup.  The counter is returned to zero by that workgroup, so the
-// workspace needs zeroing only once.
+// x_t . W[e] for each token (bf16 pairs through v_dot2c_f32_bf16), all of
+// the row's 16-byte loads issued before any arithmetic, and stores it to the
+// workspace.  Rows 0..E-1 are this layer's router, rows E..2E-1 the next
+// layer's router (lookahead), when present.
+// Phase 2 (the last workgroup to finish, found with one release/acquire
+// counter per workgroup): one wave per (token, router|lookahead) task turns
+// the logits into bf16 logits, softmax and ranking entirely in registers --
+// two experts per lane, DPP reductions, and a ballot radix-select of the top
+// k over order-preserving 16-bit keys -- then writes ids, scores, lookahead
+// ids and the slot-table lookup.  The counter is returned to zero by that
+// workgroup, so the workspace needs zeroing only once.
 //
 // Reference semantics: top_k_experts (engine_v3.py:467-473), top_k_route
 // (engine_120b.py:65-70), top_k_indices (engine_v3.py:476-483,
@@ -18,148 +22,192 @@
 
 namespace moe {
 
-
-// rank of element e among n values in LDS: count of values ranked before it
-__device__ __forceinline__ int rank_of(const float *v, int n, int e) {
-  const float me = v[e];
-  int r = 0;
-  for (int i = 0; i < n; ++i) {
-    const float o = v[i];
-    r += (o > me) || (o == me && i < e);
-  }
-  return r;
+// bf16-representable float -> 16-bit key whose unsigned order is the float
+// order (negative values flipped).
+__device__ __forceinline__ int order_key(float v) {
+  const uint32_t b = __float_as_uint(v) >> 16;
+  return (b & 0x8000u) ? (int)(~b & 0xffffu) : (int)(b | 0x8000u);
 }
 
+__device__ __forceinline__ int popc64(uint64_t m) { return __popcll(m); }
+
+// Top-kk of 2*64 candidates (e0 = lane, e1 = lane + 64; key < 0 = absent),
+// ordered by key descending then index ascending.  Returns each lane's
+// selection flags and, for selected entries, their rank.
+__device__ void select_topk(int key0, int key1, int kk, int lane, bool &sel0,
+                            bool &sel1, int &rank0, int &rank1) {
+  uint32_t prefix = 0;
+  int need = kk;
+  for (int bit = 15; bit >= 0; --bit) {
+    const uint32_t hi = (0xffffu << (bit + 1)) & 0xffffu;
+    const bool m0 = key0 >= 0 && ((uint32_t)key0 & hi) == prefix && ((key0 >> bit) & 1);
+    const bool m1 = key1 >= 0 && ((uint32_t)key1 & hi) == prefix && ((key1 >> bit) & 1);
+    const int c = popc64(__ballot(m0)) + popc64(__ballot(m1));
+    if (c >= need) prefix |= 1u << bit;
+    else need -= c;
+  }
+  const int thr = (int)prefix;
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));  // lanes below
+  const uint64_t eq0 = __ballot(key0 == thr), eq1 = __ballot(key1 == thr);
+  const int tie0 = popc64(eq0 & lt);
+  const int tie1 = popc64(eq0) + popc64(eq1 & lt);
+  sel0 = key0 > thr || (key0 == thr && tie0 < need);
+  sel1 = key1 > thr || (key1 == thr && tie1 < need);
+  // rank = selected entries ordered before this one
+  const uint64_t s0 = __ballot(sel0), s1 = __ballot(sel1);
+  rank0 = 0;
+  rank1 = 0;
+  for (uint64_t m = s0; m; m &= m - 1) {
+    const int b = __builtin_ctzll(m);
+    const int kb = __builtin_amdgcn_readlane(key0, b);
+    rank0 += kb > key0 || (kb == key0 && b < lane);
+    rank1 += kb >= key1;                       // index b < lane + 64
+  }
+  for (uint64_t m = s1; m; m &= m - 1) {
+    const int b = __builtin_ctzll(m);
+    const int kb = __builtin_amdgcn_readlane(key1, b);
+    rank0 += kb > key0;                        // index b + 64 > lane
+    rank1 += kb > key1 || (kb == key1 && b < lane);
+  }
+}
+
+template <int NIT>
+__device__ __forceinline__ void router_rows(const RouteArgs &a, int row, int lane) {
+  const bool nxt = row >= a.E;
+  const int e = nxt ? row - a.E : row;
+  const int n8 = a.D / 8;
+  const uint4 *w4 = reinterpret_cast<const uint4 *>((nxt ? a.Wn : a.W) + (int64_t)e * a.D);
+  uint4 w[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int i = lane + it * 64;
+    w[it] = (i < n8) ? load_stream16(w4 + i) : make_uint4(0, 0, 0, 0);
+  }
+  for (int t = 0; t < a.T; ++t) {
+    const uint4 *x4 = reinterpret_cast<const uint4 *>(a.x + (int64_t)t * a.D);
+    uint4 v[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int i = lane + it * 64;
+      v[it] = (i < n8) ? x4[i] : make_uint4(0, 0, 0, 0);
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      acc = dot2_bf16(w[it].x, v[it].x, acc);
+      acc = dot2_bf16(w[it].y, v[it].y, acc);
+      acc = dot2_bf16(w[it].z, v[it].z, acc);
+      acc = dot2_bf16(w[it].w, v[it].w, acc);
+    }
+    acc = group_sum<64>(acc);
+    if (lane == 0) a.logits[((nxt ? 1 : 0) * a.T + t) * a.E + e] = acc;
+  }
+}
+
+template <int NIT>
 __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nrows = a.E * (a.Wn ? 2 : 1);
   const int row = blockIdx.x * 4 + wave;
-  const int n8 = a.D / 8;  // uint4 per row
+  if (row < nrows) router_rows<NIT>(a, row, lane);
 
-  if (row < nrows) {
-    const bool nxt = row >= a.E;
-    const int e = nxt ? row - a.E : row;
-    const uint4 *w4 =
-        reinterpret_cast<const uint4 *>((nxt ? a.Wn : a.W) + (int64_t)e * a.D);
-    for (int t = 0; t < a.T; ++t) {
-      const uint4 *x4 = reinterpret_cast<const uint4 *>(a.x + (int64_t)t * a.D);
-      float acc = 0.f;
-      for (int i = lane; i < n8; i += 64) {
-        const uint4 w = w4[i], v = x4[i];
-        acc = dot2_bf16(w.x, v.x, acc);
-        acc = dot2_bf16(w.y, v.y, acc);
-        acc = dot2_bf16(w.z, v.z, acc);
-        acc = dot2_bf16(w.w, v.w, acc);
-      }
-      acc = group_sum<64>(acc);
-      if (lane == 0) a.logits[((nxt ? 1 : 0) * a.T + t) * a.E + e] = acc;
-    }
-  }
-
-  // ---- last workgroup does the selection --------------------------------
+  // ---- the last workgroup to finish does the selection ------------------
   __shared__ int s_last;
-  __threadfence();
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's logits stores have completed
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t prev = __hip_atomic_fetch_add(
-        a.counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        a.counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == gridDim.x - 1);
+    if (s_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
 
-  __shared__ float v[2][kRouteMaxE];   // ranked quantity
-  __shared__ float z[kRouteMaxE];      // bf16 logits of this layer
-  __shared__ float red[8];
-  __shared__ int sel[MOE_MAX_TOPK];
   const int E = a.E;
-  const int tid = threadIdx.x;
-  const bool router_thr = tid < E;                       // threads 0..E-1
-  const bool la_thr = a.Wn && tid >= 128 && tid - 128 < E;  // 128..128+E-1
-
-  for (int t = 0; t < a.T; ++t) {
-    float zl = -INFINITY;
-    if (router_thr) {
-      float l = __hip_atomic_load(&a.logits[t * E + tid], __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT);
-      if (a.bias) l += bf16_to_f32(a.bias[tid]);
-      zl = round_bf16(l);
-      z[tid] = zl;
+  const int ntask = a.T * (a.Wn ? 2 : 1);
+  for (int task = wave; task < ntask; task += 4) {
+    const int t = task % a.T;
+    const bool la = task >= a.T;
+    const int e0 = lane, e1 = lane + 64;
+    const float *lg = a.logits + ((la ? 1 : 0) * a.T + t) * E;
+    const uint16_t *bias = la ? a.bias_n : a.bias;
+    float z0 = -INFINITY, z1 = -INFINITY;
+    if (e0 < E) {
+      float l = __hip_atomic_load(lg + e0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (bias) l += bf16_to_f32(bias[e0]);
+      z0 = round_bf16(l);
     }
-    if (la_thr) {
-      const int e = tid - 128;
-      float l = __hip_atomic_load(&a.logits[(a.T + t) * E + e],
-                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (a.bias_n) l += bf16_to_f32(a.bias_n[e]);
-      v[1][e] = round_bf16(l);
+    if (e1 < E) {
+      float l = __hip_atomic_load(lg + e1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (bias) l += bf16_to_f32(bias[e1]);
+      z1 = round_bf16(l);
     }
-    // softmax over all E for the SOFTMAX_TOPK rule (fp32, precise)
+    // ranked quantity: bf16 softmax probabilities (SOFTMAX_TOPK router) or
+    // the bf16 logits (TOPK_SOFTMAX router, and every lookahead)
+    float v0 = z0, v1 = z1;
+    if (!la && a.mode == MOE_ROUTE_SOFTMAX_TOPK) {
+      const float m = wave_max(fmaxf(z0, z1));
+      const float x0 = (e0 < E) ? expf(z0 - m) : 0.f;
+      const float x1 = (e1 < E) ? expf(z1 - m) : 0.f;
+      const float s = group_sum<64>(x0 + x1);
+      v0 = round_bf16(x0 / s);
+      v1 = round_bf16(x1 / s);
+    }
+    const int kk = la ? a.kp : a.k;
+    bool sel0, sel1;
+    int r0, r1;
+    select_topk(e0 < E ? order_key(v0) : -1, e1 < E ? order_key(v1) : -1, kk, lane,
+                sel0, sel1, r0, r1);
+    if (la) {
+      if (sel0) a.pred[t * a.kp + r0] = e0;
+      if (sel1) a.pred[t * a.kp + r1] = e1;
+      continue;
+    }
+    // scores of the selected experts
+    float sc0 = 0.f, sc1 = 0.f;
     if (a.mode == MOE_ROUTE_SOFTMAX_TOPK) {
-      float m = zl;
-      for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-      if (lane == 0) red[wave] = m;
-      __syncthreads();
-      m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-      __syncthreads();
-      float ex = router_thr ? expf(zl - m) : 0.f;
-      float s = group_sum<64>(ex);
-      if (lane == 0) red[4 + wave] = s;
-      __syncthreads();
-      s = (red[4] + red[5]) + (red[6] + red[7]);
-      if (router_thr) v[0][tid] = round_bf16(ex / s);
-    } else if (router_thr) {
-      v[0][tid] = zl;
-    }
-    __syncthreads();
-
-    if (router_thr) {
-      const int r = rank_of(v[0], E, tid);
-      if (r < a.k) sel[r] = tid;
-    }
-    if (la_thr) {
-      const int e = tid - 128;
-      const int r = rank_of(v[1], E, e);
-      if (r < a.kp) a.pred[t * a.kp + r] = e;
-    }
-    __syncthreads();
-
-    if (tid == 0) {
-      float sc[MOE_MAX_TOPK];
-      if (a.mode == MOE_ROUTE_SOFTMAX_TOPK) {
-        float tot = 0.f;
-        for (int r = 0; r < a.k; ++r) {
-          sc[r] = v[0][sel[r]];
-          tot += sc[r];
-        }
-        if (a.renorm) {
-          tot = round_bf16(tot);
-          for (int r = 0; r < a.k; ++r) sc[r] = round_bf16(sc[r] / tot);
-        }
-      } else {
-        const float m = z[sel[0]];
-        float tot = 0.f;
-        for (int r = 0; r < a.k; ++r) {
-          sc[r] = expf(z[sel[r]] - m);
-          tot += sc[r];
-        }
-        for (int r = 0; r < a.k; ++r) sc[r] = round_bf16(sc[r] / tot);
+      sc0 = v0;
+      sc1 = v1;
+      if (a.renorm) {
+        const float tot = round_bf16(group_sum<64>((sel0 ? v0 : 0.f) + (sel1 ? v1 : 0.f)));
+        sc0 = round_bf16(v0 / tot);
+        sc1 = round_bf16(v1 / tot);
       }
-      int misses = 0;
-      for (int r = 0; r < a.k; ++r) {
-        a.ids[t * a.k + r] = sel[r];
-        a.scores[t * a.k + r] = sc[r];
-        if (a.table) {
-          const int32_t ref = a.table[sel[r]];
-          a.slot_refs[t * a.k + r] = ref;
-          misses += ref < 0;
-        }
-      }
-      if (a.miss_count && misses) atomicAdd(a.miss_count, misses);
+    } else {
+      const float m = wave_max(fmaxf(sel0 ? z0 : -INFINITY, sel1 ? z1 : -INFINITY));
+      const float x0 = sel0 ? expf(z0 - m) : 0.f;
+      const float x1 = sel1 ? expf(z1 - m) : 0.f;
+      const float s = group_sum<64>(x0 + x1);
+      sc0 = round_bf16(x0 / s);
+      sc1 = round_bf16(x1 / s);
     }
-    __syncthreads();
+    bool miss0 = false, miss1 = false;
+    if (sel0) {
+      a.ids[t * a.k + r0] = e0;
+      a.scores[t * a.k + r0] = sc0;
+      if (a.table) {
+        const int32_t ref = a.table[e0];
+        a.slot_refs[t * a.k + r0] = ref;
+        miss0 = ref < 0;
+      }
+    }
+    if (sel1) {
+      a.ids[t * a.k + r1] = e1;
+      a.scores[t * a.k + r1] = sc1;
+      if (a.table) {
+        const int32_t ref = a.table[e1];
+        a.slot_refs[t * a.k + r1] = ref;
+        miss1 = ref < 0;
+      }
+    }
+    if (a.miss_count) {
+      const int m = popc64(__ballot(miss0)) + popc64(__ballot(miss1));
+      if (lane == 0 && m) atomicAdd(a.miss_count, m);
+    }
   }
-  if (tid == 0)
+  __syncthreads();
+  if (threadIdx.x == 0)
     __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -181,7 +229,18 @@ __global__ void slot_lookup_kernel(const int32_t *table, int E,
 
 void launch_route(const RouteArgs &a, hipStream_t s) {
   const int nrows = a.E * (a.Wn ? 2 : 1);
-  hipLaunchKernelGGL(route_kernel, dim3((nrows + 3) / 4), dim3(256), 0, s, a);
+  const int nit = (a.D / 8 + 63) / 64;
+  dim3 g((nrows + 3) / 4), b(256);
+  switch (nit) {
+    case 1: hipLaunchKernelGGL(route_kernel<1>, g, b, 0, s, a); break;
+    case 2: hipLaunchKernelGGL(route_kernel<2>, g, b, 0, s, a); break;
+    case 3: hipLaunchKernelGGL(route_kernel<3>, g, b, 0, s, a); break;
+    case 4: hipLaunchKernelGGL(route_kernel<4>, g, b, 0, s, a); break;
+    case 5: hipLaunchKernelGGL(route_kernel<5>, g, b, 0, s, a); break;
+    case 6: hipLaunchKernelGGL(route_kernel<6>, g, b, 0, s, a); break;
+    case 7: hipLaunchKernelGGL(route_kernel<7>, g, b, 0, s, a); break;
+    default: hipLaunchKernelGGL(route_kernel<8>, g, b, 0, s, a); break;
+  }
 }
 
 void launch_slot_lookup(const int32_t *table, int E, const int32_t *ids, int n,

@@ -21,7 +21,7 @@ import torch
 
 from . import _lib, ops, synth
 from .geometry import Geometry
-from .pool import SlotPool
+from .pool import SlotPool, _norm_device
 
 
 class DecodeStack:
@@ -32,7 +32,7 @@ class DecodeStack:
         self.L = n_layers
         self.E = geom.n_experts
         self.k = geom.top_k
-        self.device = torch.device(device)
+        self.device = _norm_device(device)
         self.widen = widen
         self.k_pred = min(self.k * widen, self.E)
         n_rec = n_layers * self.E

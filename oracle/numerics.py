@@ -118,8 +118,10 @@ def _round(mode, v):
 # activations
 # --------------------------------------------------------------------------
 def sigmoid(z):
+    """1/(1+exp(-z)), evaluated without cancellation for either sign."""
     z = np.asarray(z, dtype=np.float64)
-    return 0.5 * (1.0 + np.tanh(0.5 * z))
+    e = np.exp(-np.abs(z))
+    return np.where(z >= 0, 1.0 / (1.0 + e), e / (1.0 + e))
 
 
 def swiglu(gate, up, mode: str = "f64"):

@@ -33,10 +33,12 @@ class PoolExhausted(RuntimeError):
 
 
 class PolicyOracle:
-    def __init__(self, n_slots: int, evict: str = "lfu", depth: int = 1):
+    def __init__(self, n_slots: int, evict: str = "lfu", depth: int = 1,
+                 window: int | None = None):
         self.n_slots = n_slots
         self.evict = evict
-        self.window = 24 * max(1, depth)            # engine_v3.py:310-311
+        # engine_v3.py:310-311; explicit `window` for small hand-made cases
+        self.window = 24 * max(1, depth) if window is None else window
         self.slot_of = {}
         self.key_of = [None] * n_slots
         self.freq = defaultdict(int)

@@ -1,0 +1,67 @@
+"""The C-ABI library loads and exports every entry point include/*.h
+declares; argument checks fail cleanly before any device call."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from moe_stream_amd import _lib
+from moe_stream_amd import geometry as G
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _declared():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(moe_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+def test_every_declared_symbol_is_exported():
+    lib = _lib.lib()
+    declared = _declared()
+    assert declared, "no declarations parsed"
+    assert declared == set(_lib.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_version_and_component_bytes():
+    lib = _lib.lib()
+    assert lib.moe_version() >= 1
+    b = (C.c_int64 * 12)()
+    g = G.QWEN3_30B_A3B
+    n = lib.moe_component_bytes(C.byref(g.c_geom()), b)
+    assert n == 9
+    assert [b[i] for i in range(9)] == [c.nbytes for c in g.components]
+    g = G.GPT_OSS_120B
+    assert lib.moe_component_bytes(C.byref(g.c_geom()), b) == 12
+    assert sum(b[i] for i in range(12)) == g.payload_bytes
+
+
+def test_argument_errors_are_reported_without_device_work():
+    lib = _lib.lib()
+    bad = G.QWEN3_30B_A3B.c_geom()
+    bad.bits = 8
+    b = (C.c_int64 * 12)()
+    assert lib.moe_component_bytes(C.byref(bad), b) == _lib.MOE_ERR_UNSUPPORTED
+    assert b"4-bit" in lib.moe_last_error()
+    g = G.QWEN3_30B_A3B.c_geom()
+    rc = lib.moe_ffn_decode(None, C.byref(g), None, None, None, 1, 8, None, None,
+                            None, 0, None)
+    assert rc == _lib.MOE_ERR_INVALID
+    rc = lib.moe_route(None, 0, 2048, None, None, 128, 0, 1, 8, None, None, None,
+                       None, 0, None, None, None, None, None, 0, None)
+    assert rc == _lib.MOE_ERR_INVALID and b"T=0" in lib.moe_last_error()
+    with pytest.raises(_lib.MoeError):
+        _lib.check(rc)
+
+
+def test_workspace_sizes():
+    lib = _lib.lib()
+    g = G.QWEN3_30B_A3B.c_geom()
+    assert lib.moe_ffn_decode_workspace(C.byref(g), 1, 8) >= 8 * 768 * 2
+    assert lib.moe_route_workspace(1, 128) >= 256 + 2 * 128 * 4

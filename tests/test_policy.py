@@ -1,0 +1,148 @@
+"""Slot-pool bookkeeping: the oracle restatement pinned by hand-derived known
+answers on tiny pools, then the native C++ policy checked against the
+oracle, call for call, on random traces.  Host only (no device calls)."""
+import numpy as np
+import pytest
+
+from moe_stream_amd.policy import NativePolicy, PoolExhausted
+from oracle.policy import PolicyOracle
+from oracle.policy import PoolExhausted as OracleExhausted
+
+
+# --------------------------------------------------- oracle known answers --
+A, B, C, D = 10, 11, 12, 13
+def test_free_list_pops_from_the_end():
+    # engine_v3.py:218,324-325: free = list(range(n)); free.pop()
+    p = PolicyOracle(3)
+    assert [p.acquire(0, [e])[0] for e in (5, 6, 7)] == [2, 1, 0]
+
+
+def _lfu_lru_scene(mode):
+    # A, B, C admitted to slots 2, 1, 0; B used 3 more times early, then A
+    # and C once each; C's acquire leaves slot 0 pinned.  A miss on D at
+    # clock 4 scans slots 1, 0, 2 (start 4 % 3, stride 7919 % 3 = 2).
+    p = PolicyOracle(3, evict=mode, window=1)
+    for e in (A, B, C):
+        p.acquire(0, [e])
+    for _ in range(3):
+        p.acquire(0, [B])
+    p.acquire(0, [A])
+    p.acquire(0, [C])
+    return p, p.acquire(0, [D])[0]
+
+
+def test_eviction_lfu_lru_asis_known_answers():
+    # LFU: B freq 4 vs A freq 2 -> A (slot 2) goes
+    p, s = _lfu_lru_scene("lfu")
+    assert s == 2 and (0, A) not in p.slot_of and (0, B) in p.slot_of
+    # LRU: B last used at 6 vs A at 7 -> B (slot 1) goes
+    p, s = _lfu_lru_scene("lru")
+    assert s == 1 and (0, B) not in p.slot_of
+    # asis: every score 0, the first candidate seen (slot 1) goes
+    p, s = _lfu_lru_scene("asis")
+    assert s == 1
+
+
+def _young_scene(window):
+    p = PolicyOracle(3, window=window)
+    p.acquire(0, [A])
+    p.acquire(0, [A])
+    p.acquire(0, [A])           # A: slot 2, born 1, freq 3
+    p.prefetch(1, [B])          # B: slot 1, born 2, freq 0
+    p.complete((1, B))
+    p.acquire(0, [C])           # C: slot 0, pinned
+    p.prefetch(1, [D])          # clock 4: scan slots 1, 0, 2
+    return p
+
+
+def test_young_entries_are_protected():
+    # window 3: B (age 2) is young, +2^30, so A (freq 3) is the victim
+    p = _young_scene(3)
+    assert p.slot_of[(1, D)] == 2 and (1, B) in p.slot_of
+    # window 1: B is old and has the lowest frequency
+    p = _young_scene(1)
+    assert p.slot_of[(1, D)] == 1 and (0, A) in p.slot_of
+
+
+def test_pending_is_not_evictable_and_exhaustion():
+    p = PolicyOracle(1)
+    p.prefetch(0, [1])                       # the only slot, in flight
+    with pytest.raises(OracleExhausted):
+        p.acquire(1, [2])
+    p2 = PolicyOracle(1)
+    p2.prefetch(0, [1])
+    p2.prefetch(2, [3])                      # silent bail
+    assert p2.stats()["bail"] == 1 and p2.stats()["issued"] == 1
+
+
+def test_hit_accounting():
+    p = PolicyOracle(4)
+    p.prefetch(1, [5])
+    assert p.acquire(1, [5]) == [3]          # waited on the pending prefetch
+    assert p.freq[(1, 5)] == 2               # touched in the loop and after the wait
+    p.prefetch(1, [6])
+    p.complete((1, 6))
+    p.acquire(1, [6])                        # completed prefetch: prefetch hit
+    p.acquire(1, [6])                        # now a cache hit
+    p.acquire(1, [7])                        # demand miss
+    assert p.stats() == dict(total=4, prefetch=2, cache=1, miss=1, bail=0, issued=2)
+    assert p.pinned == {p.slot_of[(1, 7)]}
+
+
+# ------------------------------------------------ native against oracle --
+def _run_trace(seed, n_slots, evict, n_layers=6, n_experts=24, steps=400):
+    rng = np.random.default_rng(seed)
+    o = PolicyOracle(n_slots, evict=evict, window=24)
+    n = NativePolicy(n_slots, n_layers, n_experts, evict=evict, window=24)
+    pending = []
+    for step in range(steps):
+        layer = int(rng.integers(n_layers))
+        op = rng.random()
+        if op < 0.35:
+            ex = rng.choice(n_experts, size=int(rng.integers(1, 6)), replace=False)
+            before = len(o.fills)
+            bailed_before = o.n_prefetch_bail
+            o.prefetch(layer, ex)
+            fs, fe, bailed = n.prefetch(layer, ex)
+            exp = [(k[1], s) for k, s, _ in o.fills[before:]]
+            assert list(zip(fe.tolist(), fs.tolist())) == exp, step
+            assert bailed == (o.n_prefetch_bail > bailed_before)
+            pending += [(layer, int(e)) for e in fe]
+        elif op < 0.5 and pending:
+            key = pending.pop(int(rng.integers(len(pending))))
+            o.complete(key)
+            n.complete(*key)
+        else:
+            ex = rng.choice(n_experts, size=int(rng.integers(1, 5)), replace=False)
+            try:
+                so = o.acquire(layer, ex)
+            except OracleExhausted:
+                with pytest.raises(PoolExhausted):
+                    n.acquire(layer, ex)
+                break
+            sn, miss, wait = n.acquire(layer, ex)
+            assert sn.tolist() == so, step
+        assert n.stats()["total"] == o.stats()["total"]
+        for key, slot in o.slot_of.items():
+            assert n.lookup(*key) == slot
+        assert int((n.table() >= 0).sum()) == len(o.slot_of) <= n_slots
+    so, sn = o.stats(), n.stats()
+    for k in ("total", "prefetch", "cache", "miss", "bail", "issued"):
+        assert so[k] == sn[k], k
+    assert sn["clock"] == o.clock and sn["use_clock"] == o.use_clock
+    return so
+
+
+@pytest.mark.parametrize("evict", ["lfu", "lru", "asis"])
+@pytest.mark.parametrize("n_slots", [7, 40, 150])
+def test_native_policy_matches_oracle(evict, n_slots):
+    for seed in range(3):
+        _run_trace(1000 * n_slots + seed, n_slots, evict)
+
+
+def test_native_policy_rejects_bad_keys():
+    n = NativePolicy(4, 2, 3)
+    with pytest.raises(Exception):
+        n.acquire(2, [0])
+    with pytest.raises(Exception):
+        n.prefetch(0, [3])
