@@ -155,6 +155,35 @@ int moe_route(const uint16_t *x, int32_t T, int32_t d_model,
               void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * Whole-token decode of an n_layers stack in ONE cooperative launch: for
+ * each layer l, route x[l] with W[l] (+ bias[l]) and look ahead with W[l+1],
+ * look the routed experts up in table[l] (slot refs, as moe_route), run the
+ * expert block, write y[l].  Per-layer outputs: ids/scores/slot_refs
+ * [n_layers, k], pred [n_layers, k_pred] (last layer: untouched),
+ * miss_count [n_layers] (incremented).  Equivalent to moe_route +
+ * moe_ffn_decode per layer on one stream, with the layer's phases chained by
+ * device-side counters instead of kernel boundaries, and layer l+1 starting
+ * only after y[l] is complete.
+ * epoch: 1 for the first launch on a zeroed workspace, then 2, 3, ...; after
+ * MOE_ERR_DEVICE the workspace must be zeroed and the epoch restarted.
+ * This fuses the per-layer calls of streaming_call (engine_v3.py:493-609) for
+ * a device-resident pool; it has no single counterpart in the reference.
+ */
+size_t moe_stack_workspace(const moe_geom *g, int32_t n_layers, int32_t E, int32_t k);
+/* Phase trace of moe_stack_decode: while set, each launch writes wall-clock
+ * stamps (wall_clock64 ticks) of the first 8 workgroups at the 8 phase
+ * points of every layer into device_buf ([8][n_layers][8] uint64).  NULL
+ * turns it off.  Process-wide setting. */
+int moe_stack_trace(void *device_buf, size_t bytes);
+int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_layers,
+                     int32_t E, int32_t k, const uint16_t *x, const uint16_t *W,
+                     const uint16_t *bias, int32_t mode, int32_t renorm, int32_t k_pred,
+                     const int32_t *table, uint16_t *y, int32_t *ids, float *scores,
+                     int32_t *slot_refs, int32_t *pred, int32_t *miss_count,
+                     uint32_t epoch, void *workspace, size_t workspace_bytes,
+                     void *stream);
+
+/*
  * Device-side (layer, expert) -> slot lookup for n ids (the index build of
  * engine_v3.py:550-552 against the slot table of engine_v3.py:215):
  * slot_refs[i] = table[ids[i]] for ids in [0, E); out-of-range ids give

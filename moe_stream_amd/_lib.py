@@ -33,6 +33,7 @@ EXPORTS = (
     "moe_ffn_decode_workspace", "moe_ffn_decode",
     "moe_ffn_decode_up", "moe_ffn_decode_down",
     "moe_route_workspace", "moe_route", "moe_slot_lookup",
+    "moe_stack_workspace", "moe_stack_decode", "moe_stack_trace",
     "moe_fill_slots", "moe_host_alloc", "moe_host_free",
     "moe_event_create", "moe_event_destroy", "moe_event_record",
     "moe_event_query", "moe_stream_wait_event", "moe_event_elapsed_ms",
@@ -89,6 +90,11 @@ def _declare(lib):
         "moe_route": (C.c_int, [P, I32, I32, P, P, I32, I32, I32, I32, P, P,
                                 P, P, I32, P, P, P, P, P, SZ, P]),
         "moe_slot_lookup": (C.c_int, [P, I32, P, I32, P, P, P]),
+        "moe_stack_workspace": (SZ, [C.POINTER(Geom), I32, I32, I32]),
+        "moe_stack_trace": (C.c_int, [P, SZ]),
+        "moe_stack_decode": (C.c_int, [C.POINTER(PoolView), C.POINTER(Geom), I32, I32, I32,
+                                       P, P, P, I32, I32, I32, P, P, P, P, P, P, P,
+                                       C.c_uint32, P, SZ, P]),
         "moe_fill_slots": (C.c_int, [C.POINTER(PoolView), P, I64, P, P, I32, P]),
         "moe_host_alloc": (C.c_int, [SZ, C.POINTER(C.c_void_p)]),
         "moe_host_free": (C.c_int, [P]),

@@ -274,6 +274,95 @@ int moe_route(const uint16_t *x, int32_t T, int32_t d_model, const uint16_t *W,
   return MOE_OK;
 }
 
+static uint64_t *g_stack_trace = nullptr;
+static size_t g_stack_trace_bytes = 0;
+
+int moe_stack_trace(void *device_buf, size_t bytes) {
+  g_stack_trace = static_cast<uint64_t *>(device_buf);
+  g_stack_trace_bytes = device_buf ? bytes : 0;
+  return MOE_OK;
+}
+
+size_t moe_stack_workspace(const moe_geom *g, int32_t n_layers, int32_t E, int32_t k) {
+  if (!g || n_layers <= 0 || E <= 0 || k <= 0) return 0;
+  const size_t counters = (size_t)n_layers * moe::kCountersPerLayer * moe::kCounterWords * 4;
+  const size_t logits = ((size_t)2 * E * 4 + 255) & ~(size_t)255;
+  const size_t h = ((size_t)k * g->d_ff * 4 + 255) & ~(size_t)255;
+  return counters + logits + h;
+}
+
+int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_layers,
+                     int32_t E, int32_t k, const uint16_t *x, const uint16_t *W,
+                     const uint16_t *bias, int32_t mode, int32_t renorm, int32_t k_pred,
+                     const int32_t *table, uint16_t *y, int32_t *ids, float *scores,
+                     int32_t *slot_refs, int32_t *pred, int32_t *miss_count,
+                     uint32_t epoch, void *workspace, size_t workspace_bytes,
+                     void *stream) {
+  moe::PoolArgs pa;
+  int rc = make_pool_args(pool, g, &pa);
+  if (rc) return rc;
+  const moe::StackLaunch *S = moe::find_stack(g->d_model, g->d_ff, k, g->has_proj_bias);
+  if (!S)
+    return fail(MOE_ERR_UNSUPPORTED,
+                "no persistent decode kernel for d_model=%d d_ff=%d k=%d proj_bias=%d",
+                g->d_model, g->d_ff, k, g->has_proj_bias);
+  if (n_layers <= 0) return fail(MOE_ERR_INVALID, "n_layers=%d", n_layers);
+  if (E <= 0 || E > moe::kRouteMaxE || 2 * E > S->nwg)
+    return fail(MOE_ERR_INVALID, "E=%d outside [1, %d]", E, moe::kRouteMaxE);
+  if (mode != MOE_ROUTE_SOFTMAX_TOPK && mode != MOE_ROUTE_TOPK_SOFTMAX)
+    return fail(MOE_ERR_INVALID, "unknown routing mode %d", mode);
+  if (k_pred <= 0 || k_pred > E || k_pred > 64)
+    return fail(MOE_ERR_INVALID, "k_pred=%d outside [1, min(E, 64)]", k_pred);
+  if (g->act != MOE_ACT_SWIGLU && g->act != MOE_ACT_SWIGLU_CLAMP)
+    return fail(MOE_ERR_INVALID, "unknown activation %d", g->act);
+  if (!x || !W || !table || !y || !ids || !scores || !slot_refs || !pred || !miss_count ||
+      !workspace)
+    return fail(MOE_ERR_INVALID, "NULL argument");
+  if (!aligned(x, 16) || !aligned(W, 16) || !aligned(workspace, 256))
+    return fail(MOE_ERR_INVALID, "x/W must be 16-byte and workspace 256-byte aligned");
+  if (workspace_bytes < moe_stack_workspace(g, n_layers, E, k))
+    return fail(MOE_ERR_INVALID, "workspace %zu < %zu bytes", workspace_bytes,
+                moe_stack_workspace(g, n_layers, E, k));
+  if (epoch == 0) return fail(MOE_ERR_INVALID, "epoch must start at 1");
+  char *ws = static_cast<char *>(workspace);
+  moe::StackArgs a;
+  a.pa = pa;
+  a.x = x;
+  a.W = W;
+  a.bias = bias;
+  a.table = table;
+  a.y = y;
+  a.ids = ids;
+  a.scores = scores;
+  a.refs_out = slot_refs;
+  a.pred = pred;
+  a.miss = miss_count;
+  a.cnt = reinterpret_cast<uint32_t *>(ws);
+  ws += (size_t)n_layers * moe::kCountersPerLayer * moe::kCounterWords * 4;
+  a.logits = reinterpret_cast<float *>(ws);
+  ws += ((size_t)2 * E * 4 + 255) & ~(size_t)255;
+  a.h = reinterpret_cast<float *>(ws);
+  a.L = n_layers;
+  a.E = E;
+  a.kp = k_pred;
+  a.mode = mode;
+  a.renorm = renorm;
+  a.act = g->act;
+  a.alpha = g->alpha;
+  a.limit = g->limit;
+  a.epoch = epoch;
+  a.trace = nullptr;
+  if (g_stack_trace) {
+    const size_t need = (size_t)moe::kTraceWGs * n_layers * moe::kTracePoints * 8;
+    if (g_stack_trace_bytes < need)
+      return fail(MOE_ERR_INVALID, "trace buffer %zu < %zu bytes", g_stack_trace_bytes, need);
+    a.trace = g_stack_trace;
+  }
+  (void)hipGetLastError();
+  MOE_HIP(moe::launch_stack(S, a, static_cast<hipStream_t>(stream)));
+  return MOE_OK;
+}
+
 int moe_slot_lookup(const int32_t *table, int32_t E, const int32_t *ids,
                     int32_t n, int32_t *slot_refs, int32_t *miss_count,
                     void *stream) {

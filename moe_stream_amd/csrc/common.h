@@ -99,10 +99,14 @@ __device__ __forceinline__ float group_sum(float v) {
   if (SG >= 4) v += dpp_f<kDppQuadXor2>(v);
   if (SG >= 8) v += dpp_f<kDppHalfMirror>(v);
   if (SG >= 16) v += dpp_f<kDppMirror>(v);
-  if (SG >= 32) v += swz_xor16_f(v);
-  if (SG >= 64)
-    v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
-        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  if (SG == 32) v += swz_xor16_f(v);
+  if (SG >= 64) {  // the four 16-lane rows through readlanes: a uniform value
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    v = (a + b) + (c + d);
+  }
   return v;
 }
 
@@ -111,9 +115,21 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f<kDppQuadXor2>(v));
   v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
   v = fmaxf(v, dpp_f<kDppMirror>(v));
-  v = fmaxf(v, swz_xor16_f(v));
-  return fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)),
-               __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)));
+  const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+__device__ __forceinline__ int wave_max_i(int v) {
+  v = max(v, dpp_i<kDppQuadXor1>(v));
+  v = max(v, dpp_i<kDppQuadXor2>(v));
+  v = max(v, dpp_i<kDppHalfMirror>(v));
+  v = max(v, dpp_i<kDppMirror>(v));
+  const int a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+  const int c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+  return max(max(a, b), max(c, d));
 }
 
 // Pool view passed to kernels by value.

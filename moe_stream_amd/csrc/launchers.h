@@ -51,6 +51,15 @@ struct RouteArgs {
   int T, D, E, mode, renorm, k, kp;
 };
 void launch_route(const RouteArgs &a, hipStream_t s);
+
+// ---- whole-token persistent decode (stack_decode.hip) ---------------------
+struct StackArgs;
+struct StackLaunch {
+  int d_model, d_ff, k, has_bias, nwg;
+  const void *func;
+};
+const StackLaunch *find_stack(int d_model, int d_ff, int k, int has_bias);
+hipError_t launch_stack(const StackLaunch *S, StackArgs &a, hipStream_t s);
 void launch_slot_lookup(const int32_t *table, int E, const int32_t *ids, int n,
                         int32_t *refs, int32_t *miss_count, hipStream_t s);
 

@@ -2,5 +2,6 @@
 // device error word without relocatable device code).
 #include "ffn_decode.hip"
 #include "route.hip"
+#include "stack_decode.hip"
 #include "capi.hip"
 #include "policy.cpp"

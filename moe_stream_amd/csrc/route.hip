@@ -33,41 +33,20 @@ __device__ __forceinline__ int popc64(uint64_t m) { return __popcll(m); }
 
 // Top-kk of 2*64 candidates (e0 = lane, e1 = lane + 64; key < 0 = absent),
 // ordered by key descending then index ascending.  Returns each lane's
-// selection flags and, for selected entries, their rank.
+// selection flags and, for selected entries, their rank.  Key and inverted
+// index are packed into one int, so a single integer max picks the largest
+// key and, among equal keys, the smallest index; kk rounds of a DPP wave max.
 __device__ void select_topk(int key0, int key1, int kk, int lane, bool &sel0,
                             bool &sel1, int &rank0, int &rank1) {
-  uint32_t prefix = 0;
-  int need = kk;
-  for (int bit = 15; bit >= 0; --bit) {
-    const uint32_t hi = (0xffffu << (bit + 1)) & 0xffffu;
-    const bool m0 = key0 >= 0 && ((uint32_t)key0 & hi) == prefix && ((key0 >> bit) & 1);
-    const bool m1 = key1 >= 0 && ((uint32_t)key1 & hi) == prefix && ((key1 >> bit) & 1);
-    const int c = popc64(__ballot(m0)) + popc64(__ballot(m1));
-    if (c >= need) prefix |= 1u << bit;
-    else need -= c;
-  }
-  const int thr = (int)prefix;
-  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));  // lanes below
-  const uint64_t eq0 = __ballot(key0 == thr), eq1 = __ballot(key1 == thr);
-  const int tie0 = popc64(eq0 & lt);
-  const int tie1 = popc64(eq0) + popc64(eq1 & lt);
-  sel0 = key0 > thr || (key0 == thr && tie0 < need);
-  sel1 = key1 > thr || (key1 == thr && tie1 < need);
-  // rank = selected entries ordered before this one
-  const uint64_t s0 = __ballot(sel0), s1 = __ballot(sel1);
-  rank0 = 0;
-  rank1 = 0;
-  for (uint64_t m = s0; m; m &= m - 1) {
-    const int b = __builtin_ctzll(m);
-    const int kb = __builtin_amdgcn_readlane(key0, b);
-    rank0 += kb > key0 || (kb == key0 && b < lane);
-    rank1 += kb >= key1;                       // index b < lane + 64
-  }
-  for (uint64_t m = s1; m; m &= m - 1) {
-    const int b = __builtin_ctzll(m);
-    const int kb = __builtin_amdgcn_readlane(key1, b);
-    rank0 += kb > key0;                        // index b + 64 > lane
-    rank1 += kb > key1 || (kb == key1 && b < lane);
+  int p0 = key0 >= 0 ? (key0 << 8) | (255 - lane) : -1;
+  int p1 = key1 >= 0 ? (key1 << 8) | (255 - (lane + 64)) : -1;
+  sel0 = sel1 = false;
+  rank0 = rank1 = 0;
+  for (int r = 0; r < kk; ++r) {
+    const int m = wave_max_i(max(p0, p1));
+    if (m < 0) break;                        // fewer candidates than kk
+    if (p0 == m) { sel0 = true; rank0 = r; p0 = -1; }
+    if (p1 == m) { sel1 = true; rank1 = r; p1 = -1; }
   }
 }
 
@@ -100,7 +79,10 @@ __device__ __forceinline__ void router_rows(const RouteArgs &a, int row, int lan
       acc = dot2_bf16(w[it].w, v[it].w, acc);
     }
     acc = group_sum<64>(acc);
-    if (lane == 0) a.logits[((nxt ? 1 : 0) * a.T + t) * a.E + e] = acc;
+    // device-scope store: read back by the last workgroup on another CU/XCD
+    if (lane == 0)
+      __hip_atomic_store(&a.logits[((nxt ? 1 : 0) * a.T + t) * a.E + e], acc,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -112,14 +94,16 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   if (row < nrows) router_rows<NIT>(a, row, lane);
 
   // ---- the last workgroup to finish does the selection ------------------
+  // The logits travel through device-scope (sc1) stores and loads, coherent
+  // across XCDs without L2 writeback/invalidate; every wave waits for its
+  // stores to complete before the workgroup's one relaxed increment.
   __shared__ int s_last;
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's logits stores have completed
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(
-        a.counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == gridDim.x - 1);
-    if (s_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
   if (!s_last) return;

@@ -121,6 +121,48 @@ class DecodeStack:
         else:
             self.token_eager()
 
+    # -- one launch per token ---------------------------------------------
+    def persistent_supported(self) -> bool:
+        import ctypes as C
+        L = _lib.lib()
+        g = self.geom.c_geom()
+        return L.moe_stack_workspace(C.byref(g), self.L, self.E, self.k) > 0 and \
+            (self.geom.d_model, self.geom.d_ff, self.k, self.geom.has_proj_bias) in \
+            {(2048, 768, 8, False)}
+
+    def _persistent_buffers(self):
+        import ctypes as C
+        g = self.geom.c_geom()
+        n = _lib.lib().moe_stack_workspace(C.byref(g), self.L, self.E, self.k)
+        dev = self.device
+        self.p_ws = torch.zeros(n, dtype=torch.uint8, device=dev)
+        self.p_epoch = 0
+        self.p_ids = torch.zeros((self.L, self.k), dtype=torch.int32, device=dev)
+        self.p_scores = torch.zeros((self.L, self.k), dtype=torch.float32, device=dev)
+        self.p_refs = torch.zeros((self.L, self.k), dtype=torch.int32, device=dev)
+        self.p_pred = torch.zeros((self.L, self.k_pred), dtype=torch.int32, device=dev)
+        self.p_miss = torch.zeros((self.L,), dtype=torch.int32, device=dev)
+        self.p_y = torch.zeros((self.L, self.geom.d_model), dtype=torch.bfloat16, device=dev)
+
+    def token_persistent(self, x_tok: torch.Tensor, stream=None):
+        """All layers of one token in one cooperative launch.  x_tok: bf16
+        [n_layers, d_model]; outputs in p_y, p_ids, p_scores, p_refs, p_pred,
+        p_miss."""
+        import ctypes as C
+        if not hasattr(self, "p_ws"):
+            self._persistent_buffers()
+        x_tok = x_tok.contiguous()
+        self.p_epoch += 1
+        g = self.geom.c_geom()
+        b = self.bias.data_ptr() if self.bias is not None else None
+        _lib.check(_lib.lib().moe_stack_decode(
+            C.byref(self.pool.c_view()), C.byref(g), self.L, self.E, self.k,
+            x_tok.data_ptr(), self.W.data_ptr(), b, self.geom.routing,
+            int(self.geom.norm_topk_prob), self.k_pred, self.table.data_ptr(),
+            self.p_y.data_ptr(), self.p_ids.data_ptr(), self.p_scores.data_ptr(),
+            self.p_refs.data_ptr(), self.p_pred.data_ptr(), self.p_miss.data_ptr(),
+            self.p_epoch, self.p_ws.data_ptr(), self.p_ws.numel(), _lib.stream_ptr(stream)))
+
     # -- bookkeeping --------------------------------------------------------
     def expert_bytes_per_token(self) -> int:
         return self.L * self.k * self.geom.payload_bytes

@@ -1,0 +1,64 @@
+"""The whole-token persistent decode against the per-layer launches: same
+routed ids, scores, slot refs, lookahead ids, miss counts and bit-identical
+layer outputs, over several consecutive tokens (the epoch counters), plus one
+layer against the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from moe_stream_amd import geometry as G
+from moe_stream_amd import ops, synth
+from moe_stream_amd.stack import DecodeStack
+from oracle import layout as OL
+from oracle import numerics as N
+
+from helpers import TOL, bf16_bits, bf16_values
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def stack():
+    geom = G.QWEN3_30B_A3B
+    # 6 layers, a pool of 384 slots (half the pairs): refs of both signs
+    return DecodeStack(geom, 6, 384, "cuda", seed=20260601, zipf_s=1.1)
+
+
+def test_persistent_equals_per_layer(stack):
+    xs = synth.hidden_states(4, stack.L, 2048, "cuda", 20260602)
+    for t in range(xs.shape[0]):
+        stack.run_token(xs[t], use_graph=False)
+        ids, sc, refs, pred = stack.routed()
+        y_ref = stack.y.clone()
+        stack.token_persistent(xs[t])
+        torch.cuda.synchronize()
+        ops.check_device_error()
+        np.testing.assert_array_equal(stack.p_ids.cpu().numpy(), ids)
+        np.testing.assert_array_equal(stack.p_scores.cpu().numpy(), sc)
+        np.testing.assert_array_equal(stack.p_refs.cpu().numpy(), refs)
+        np.testing.assert_array_equal(stack.p_pred.cpu().numpy()[:-1], pred[:-1])
+        assert torch.equal(stack.p_y, y_ref), t
+    assert int(stack.p_miss.sum()) > 0          # some experts read from the store
+
+
+def test_persistent_layer_against_oracle(stack):
+    xs = synth.hidden_states(1, stack.L, 2048, "cuda", 20260603)
+    stack.token_persistent(xs[0])
+    torch.cuda.synchronize()
+    Wb, bb = bf16_bits(stack.W), bf16_bits(stack.bias)
+    store = stack.store
+    for l in (0, stack.L - 1):
+        x64 = bf16_values(xs[0, l])
+        z = N.router_logits(x64, Wb[l], bb[l], "mlx")
+        ref_ids, _, ranked = N.top_k_experts(z, 8, True, "mlx")
+        ids = stack.p_ids[l].cpu().numpy()
+        assert N.ids_match(ranked, ref_ids, ids)
+        sc = stack.p_scores[l].cpu().numpy().astype(np.float64)
+        exps = [OL.split_record(store[l * 128 + int(e)].cpu().numpy(), 2048, 768, False)
+                for e in ids]
+        ref = N.moe_block(x64, exps, sc, "qwen3", "mlx")
+        assert N.rel_err(bf16_values(stack.p_y[l]), ref) < TOL
+        if l + 1 < stack.L:
+            zn = N.router_logits(x64, Wb[l + 1], bb[l + 1], "mlx")
+            want = N.top_k_indices(zn, stack.k_pred)
+            assert N.ids_match(zn, want, stack.p_pred[l].cpu().numpy())
