@@ -33,7 +33,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--tokens", type=int, default=64)
     ap.add_argument("--workload", default="qwen3-48l",
-                    choices=["qwen3-48l", "gptoss-36l"])
+                    choices=["qwen3-48l", "gptoss-36l", "qwen3-prefill"],
+                    help="qwen3-prefill: 512 tokens per layer through the grouped "
+                         "MFMA path (a secondary measurement, not the headline)")
     ap.add_argument("--mode", default="persistent", choices=["persistent", "graph", "eager"],
                     help="persistent: one launch per token; graph/eager: 3 launches per layer")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -63,6 +65,94 @@ def workload(args, device):
                "activation": "clamped swiglu a=1.702 limit=7", "global_batch": 1,
                "tokens_per_step": args.tokens}
     return stack, cfg
+
+
+MFMA_BF16_PEAK_TFS = 2500.0   # MI355X dense bf16 MFMA
+
+
+def prefill(args):
+    """48 layers x 512 tokens through the grouped MFMA path: per layer the
+    many-token router and the grouped expert block.  One step = the 512
+    tokens through all 48 layers.  Reports tokens/s, the expert block's
+    algorithmic TFLOP/s against the bf16 MFMA peak, and the bytes of the
+    distinct experts the step reads against HBM peak."""
+    import torch
+    from moe_stream_amd import geometry as G
+    from moe_stream_amd import ops, synth
+    from moe_stream_amd.stack import PrefillStack
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    T, L, slots = args.tokens if args.tokens != 64 else 512, 48, 3072
+    geom = G.QWEN3_30B_A3B
+    stack = PrefillStack(geom, L, slots, T, dev, zipf_s=1.1)
+    xs = synth.hidden_states(T, L, geom.d_model, dev, synth.SEED_BASE + 300)  # [T, L, D]
+    x_step = xs.transpose(0, 1).contiguous()                                   # [L, T, D]
+    stack.x_in.copy_(x_step)
+    s = torch.cuda.current_stream()
+    ev = []
+
+    def step(timed=False):
+        for Lx in range(L):
+            if timed:
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            nxt = Lx + 1 < L
+            bufs = stack.bufs[Lx]
+            ops.route(stack.x_in[Lx], stack.W[Lx], stack.bias[Lx], geom.routing,
+                      geom.norm_topk_prob, stack.k,
+                      W_next=stack.W[Lx + 1] if nxt else None,
+                      bias_next=stack.bias[Lx + 1] if nxt else None,
+                      k_pred=stack.k_pred, table=stack.table[Lx], bufs=bufs,
+                      workspace=stack.route_ws)
+            if timed:
+                a.record(s)
+            ops.ffn_grouped(stack.pool, bufs.slot_refs, bufs.scores, stack.x_in[Lx],
+                            out=stack.y[Lx], workspace=stack.ffn_ws)
+            if timed:
+                b.record(s)
+                ev.append((a, b))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step(timed=True)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ops.check_device_error()
+    gpu_ms = e0.elapsed_time(e1)
+    counts = stack.routed_counts()                     # [L, E] pairs per expert
+    pairs = int(counts.sum())
+    distinct = int((counts > 0).sum())
+    flops = 2.0 * pairs * geom.d_model * geom.d_ff * 3   # gate, up, down
+    block_ms = np.array([a.elapsed_time(b) for a, b in ev]).reshape(args.steps, L)
+    block_s = block_ms.sum(1).mean() / 1e3
+    tflops = flops / block_s / 1e12
+    wbytes = distinct * geom.payload_bytes
+    out = {"metric": "MoE prefill tok/s (512 tokens x 48 layers, grouped bf16 MFMA)",
+           "value": round(T * args.steps / (gpu_ms / 1e3), 1), "unit": "tok/s",
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(gpu_ms / args.steps, 4), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+           "config": {"workload": "qwen3-30b-a3b-moe-stack-prefill", "layers": L,
+                      "tokens_per_layer": T, "top_k": stack.k, "pool_slots": slots,
+                      "router_bias": "zipf(1.1) log-popularity",
+                      "pairs_per_layer": pairs // L,
+                      "distinct_experts_per_layer": round(distinct / L, 1),
+                      "max_pairs_per_expert": int(counts.max()),
+                      "parallelism": "none (1 GPU)"},
+           "roofline": {"bound": "mfma", "kernel": "expert block (group + gate/up + "
+                        "down + combine)", "achieved": round(tflops, 2),
+                        "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s",
+                        "frac": round(tflops / MFMA_BF16_PEAK_TFS, 4), "traffic": None,
+                        "flops_per_step": flops,
+                        "avg_block_us": round(float(block_ms.mean()) * 1e3, 2)},
+           "expert_weight_GBs": round(wbytes / block_s / 1e9, 1),
+           "wall_s": round(wall, 3)}
+    print(json.dumps(out), flush=True)
 
 
 def time_dominant_kernel(stack, xs, n_tok):
@@ -167,6 +257,8 @@ def main():
         print("bench.py measures one GPU: the expert path at bs=1 does not shard "
               "(see the sharding note in DESIGN.md); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "qwen3-prefill":
+        return prefill(args)
     import torch
     from moe_stream_amd import synth
     dev = torch.device("cuda:0")

@@ -124,6 +124,30 @@ int moe_ffn_decode_down(const moe_pool_view *pool, const moe_geom *g,
                         size_t workspace_bytes, void *stream);
 
 /*
+ * Multi-token (prefill / batched) expert block: the same contract as
+ * moe_ffn_decode -- y_t = sum_j scores[t*k+j] * down_j(act(gate_j(x_t),
+ * up_j(x_t))) with expert j read via slot_refs[t*k+j] -- computed by
+ * grouping the T*k pairs per slot reference and running each group as a bf16
+ * MFMA contraction over the 4-bit codes (fp32 accumulation).  For T*k well
+ * above the number of distinct slots, where an expert's weights serve many
+ * tokens per read.  Results are deterministic and independent of how pairs
+ * group.
+ *
+ * Replaces the batched (prefill) mx.gather_qmm calls, swiglu and weighted sum
+ * of engine_v3.py:588-600 and engine_120b.py:132-145.
+ *
+ * Limits: pool->n_slots + (store ? pool->n_records : 0) <= 16256; T*k <=
+ * 2^24.  workspace: at least moe_ffn_grouped_workspace() bytes (no zeroing
+ * needed).
+ */
+size_t moe_ffn_grouped_workspace(const moe_geom *g, int32_t T, int32_t k);
+int moe_ffn_grouped(const moe_pool_view *pool, const moe_geom *g,
+                    const int32_t *slot_refs, const float *scores,
+                    const uint16_t *x, int32_t T, int32_t k,
+                    uint16_t *out_bf16, float *out_f32,
+                    void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * Router + top-k (+ lookahead + slot lookup) for T tokens in one launch.
  *   logits = x @ W.T (+ bias), materialised as bf16;
  *   mode SOFTMAX_TOPK: probs = bf16(softmax(logits)); top-k of probs; scores
@@ -132,8 +156,10 @@ int moe_ffn_decode_down(const moe_pool_view *pool, const moe_geom *g,
  *   mode TOPK_SOFTMAX: top-k of logits; scores = bf16(softmax(selected))
  *     (top_k_route, engine_120b.py:65-70).
  * ids are ranked (value descending, ties to the lower expert id).
- * Limits: T <= 16, E <= 128, d_model <= 4096 (multiple of 8), k <= 16,
- *   k_pred <= 64.
+ * Limits: E <= 128, k <= 16, k_pred <= 64; T <= 16 with d_model <= 4096 (a
+ *   multiple of 8) runs one fused launch; T > 16 (prefill, up to 2^20
+ *   tokens) needs d_model a multiple of 32 and runs a bf16 MFMA logits
+ *   kernel, then the same selection.
  * Lookahead (W_next != NULL): pred_ids[t, 0..k_pred) = top-k_pred of the raw
  *   bf16 logits of x @ W_next.T (+ bias_next) (top_k_indices,
  *   engine_v3.py:476-483, engine_120b.py:73-75).

@@ -210,6 +210,53 @@ int moe_ffn_decode(const moe_pool_view *pool, const moe_geom *g,
   return MOE_OK;
 }
 
+size_t moe_ffn_grouped_workspace(const moe_geom *g, int32_t T, int32_t k) {
+  if (!g || T <= 0 || k <= 0 || (int64_t)T * k > (1 << 24) || g->d_model <= 0 ||
+      g->d_ff <= 0)
+    return 0;
+  return moe::grouped_ws(T, k, g->d_model, g->d_ff).total;
+}
+
+int moe_ffn_grouped(const moe_pool_view *pool, const moe_geom *g,
+                    const int32_t *slot_refs, const float *scores, const uint16_t *x,
+                    int32_t T, int32_t k, uint16_t *out_bf16, float *out_f32,
+                    void *workspace, size_t workspace_bytes, void *stream) {
+  moe::PoolArgs pa;
+  int rc = make_pool_args(pool, g, &pa);
+  if (rc) return rc;
+  if (T <= 0) return fail(MOE_ERR_INVALID, "T=%d must be positive", T);
+  if (k <= 0 || k > MOE_MAX_TOPK)
+    return fail(MOE_ERR_INVALID, "k=%d outside [1, %d]", k, MOE_MAX_TOPK);
+  if ((int64_t)T * k > (1 << 24))
+    return fail(MOE_ERR_INVALID, "T*k=%lld above 2^24", (long long)T * k);
+  if (!slot_refs || !scores || !x || !workspace)
+    return fail(MOE_ERR_INVALID, "NULL slot_refs/scores/x/workspace");
+  if (!out_bf16 && !out_f32) return fail(MOE_ERR_INVALID, "no output buffer");
+  if (!aligned(x, 16) || !aligned(workspace, 256) || (out_bf16 && !aligned(out_bf16, 8)) ||
+      (out_f32 && !aligned(out_f32, 16)))
+    return fail(MOE_ERR_INVALID,
+                "x/out_f32 must be 16-byte, out_bf16 8-byte, workspace 256-byte aligned");
+  if (g->act != MOE_ACT_SWIGLU && g->act != MOE_ACT_SWIGLU_CLAMP)
+    return fail(MOE_ERR_INVALID, "unknown activation %d", g->act);
+  if ((int64_t)pa.n_slots + pa.n_records > moe::kGroupMaxKeys)
+    return fail(MOE_ERR_UNSUPPORTED, "n_slots + n_records = %lld above %d",
+                (long long)pa.n_slots + pa.n_records, moe::kGroupMaxKeys);
+  const moe::GroupedLaunch *G = moe::find_grouped(g->d_model, g->d_ff, g->has_proj_bias);
+  if (!G)
+    return fail(MOE_ERR_UNSUPPORTED,
+                "no grouped kernel compiled for d_model=%d d_ff=%d proj_bias=%d", g->d_model,
+                g->d_ff, g->has_proj_bias);
+  const size_t need = moe_ffn_grouped_workspace(g, T, k);
+  if (workspace_bytes < need)
+    return fail(MOE_ERR_INVALID, "workspace %zu < %zu bytes", workspace_bytes, need);
+  (void)hipGetLastError();
+  moe::launch_grouped(G, pa, slot_refs, scores, x, T, k, out_bf16, out_f32,
+                      static_cast<char *>(workspace), g->act, g->alpha, g->limit,
+                      static_cast<hipStream_t>(stream));
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
 size_t moe_route_workspace(int32_t T, int32_t E) {
   if (T <= 0 || E <= 0) return 0;
   // counter word (padded to 256 B) + logits [2][T][E] fp32
@@ -222,12 +269,14 @@ int moe_route(const uint16_t *x, int32_t T, int32_t d_model, const uint16_t *W,
               const uint16_t *bias_next, int32_t k_pred, int32_t *pred_ids,
               const int32_t *table, int32_t *slot_refs, int32_t *miss_count,
               void *workspace, size_t workspace_bytes, void *stream) {
-  if (T <= 0 || T > moe::kRouteMaxT)
-    return fail(MOE_ERR_INVALID, "T=%d outside [1, %d]", T, moe::kRouteMaxT);
+  if (T <= 0 || T > (1 << 20)) return fail(MOE_ERR_INVALID, "T=%d outside [1, 2^20]", T);
   if (E <= 0 || E > moe::kRouteMaxE)
     return fail(MOE_ERR_INVALID, "E=%d outside [1, %d]", E, moe::kRouteMaxE);
-  if (d_model <= 0 || d_model % 8 || d_model > 4096)
+  if (T <= moe::kRouteMaxT && (d_model <= 0 || d_model % 8 || d_model > 4096))
     return fail(MOE_ERR_INVALID, "d_model=%d must be a multiple of 8 in [8, 4096]", d_model);
+  if (T > moe::kRouteMaxT && (d_model <= 0 || d_model % 32))
+    return fail(MOE_ERR_INVALID, "T=%d > %d needs d_model (%d) a positive multiple of 32", T,
+                moe::kRouteMaxT, d_model);
   if (k <= 0 || k > MOE_MAX_TOPK || k > E)
     return fail(MOE_ERR_INVALID, "k=%d outside [1, min(E, %d)]", k, MOE_MAX_TOPK);
   if (mode != MOE_ROUTE_SOFTMAX_TOPK && mode != MOE_ROUTE_TOPK_SOFTMAX)

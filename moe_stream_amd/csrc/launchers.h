@@ -52,6 +52,28 @@ struct RouteArgs {
 };
 void launch_route(const RouteArgs &a, hipStream_t s);
 
+// ---- multi-token grouped MFMA expert block (grouped.hip) ------------------
+constexpr int kGroupMaxKeys = 16256;    // n_slots + n_records: LDS histogram <= 64 KiB
+constexpr int kGroupedMaxWGs = 2048;    // grid cap; workgroups loop over items
+struct GroupedLaunch {
+  int d_model, d_ff, has_bias;
+  void (*gate_up)(dim3, hipStream_t, const PoolArgs &, const uint16_t *, int,
+                  const int32_t *, const int4 *, const int32_t *, uint16_t *, int, float,
+                  float);
+  void (*down)(dim3, hipStream_t, const PoolArgs &, const uint16_t *, const float *,
+               const int32_t *, const int4 *, const int32_t *, float *);
+};
+struct GroupedWs {
+  int64_t max_tiles;
+  size_t off_perm, off_tiles, off_ntiles, off_h, off_yp, total;
+};
+const GroupedLaunch *find_grouped(int d_model, int d_ff, int has_bias);
+GroupedWs grouped_ws(int64_t T, int k, int D, int F);
+void launch_grouped(const GroupedLaunch *G, const PoolArgs &pa, const int32_t *refs,
+                    const float *scores, const uint16_t *x, int T, int k, uint16_t *out,
+                    float *out32, char *ws, int act, float alpha, float limit,
+                    hipStream_t s);
+
 // ---- whole-token persistent decode (stack_decode.hip) ---------------------
 struct StackArgs;
 struct StackLaunch {

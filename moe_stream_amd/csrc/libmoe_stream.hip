@@ -2,6 +2,7 @@
 // device error word without relocatable device code).
 #include "ffn_decode.hip"
 #include "route.hip"
+#include "grouped.hip"
 #include "stack_decode.hip"
 #include "capi.hip"
 #include "policy.cpp"

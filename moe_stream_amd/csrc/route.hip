@@ -5,13 +5,16 @@
 // the row's 16-byte loads issued before any arithmetic, and stores it to the
 // workspace.  Rows 0..E-1 are this layer's router, rows E..2E-1 the next
 // layer's router (lookahead), when present.
-// Phase 2 (the last workgroup to finish, found with one release/acquire
-// counter per workgroup): one wave per (token, router|lookahead) task turns
+// Phase 2 (the last workgroup to finish, found with one relaxed device-scope
+// counter increment per workgroup after its logits stores have completed):
+// one wave per (token, router|lookahead) task turns
 // the logits into bf16 logits, softmax and ranking entirely in registers --
 // two experts per lane, DPP reductions, and a ballot radix-select of the top
 // k over order-preserving 16-bit keys -- then writes ids, scores, lookahead
 // ids and the slot-table lookup.  The counter is returned to zero by that
 // workgroup, so the workspace needs zeroing only once.
+// Many tokens (prefill, T > 16): the logits come from a bf16 MFMA kernel and a
+// second kernel runs the same per-task selection.
 //
 // Reference semantics: top_k_experts (engine_v3.py:467-473), top_k_route
 // (engine_120b.py:65-70), top_k_indices (engine_v3.py:476-483,
@@ -47,6 +50,93 @@ __device__ void select_topk(int key0, int key1, int kk, int lane, bool &sel0,
     if (m < 0) break;                        // fewer candidates than kk
     if (p0 == m) { sel0 = true; rank0 = r; p0 = -1; }
     if (p1 == m) { sel1 = true; rank1 = r; p1 = -1; }
+  }
+}
+
+// One selection task on one wave: task < T is token t's routing (ids, scores,
+// slot refs, misses), task >= T token t's lookahead prediction.  The logits
+// are read with device-scope loads: in route_kernel another workgroup of the
+// same launch wrote them.
+__device__ void select_task(const RouteArgs &a, int task, int lane) {
+  const int E = a.E;
+  const int t = task % a.T;
+  const bool la = task >= a.T;
+  const int e0 = lane, e1 = lane + 64;
+  const float *lg = a.logits + ((int64_t)(la ? 1 : 0) * a.T + t) * E;
+  const uint16_t *bias = la ? a.bias_n : a.bias;
+  float z0 = -INFINITY, z1 = -INFINITY;
+  if (e0 < E) {
+    float l = __hip_atomic_load(lg + e0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (bias) l += bf16_to_f32(bias[e0]);
+    z0 = round_bf16(l);
+  }
+  if (e1 < E) {
+    float l = __hip_atomic_load(lg + e1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (bias) l += bf16_to_f32(bias[e1]);
+    z1 = round_bf16(l);
+  }
+  // ranked quantity: bf16 softmax probabilities (SOFTMAX_TOPK router) or
+  // the bf16 logits (TOPK_SOFTMAX router, and every lookahead)
+  float v0 = z0, v1 = z1;
+  if (!la && a.mode == MOE_ROUTE_SOFTMAX_TOPK) {
+    const float m = wave_max(fmaxf(z0, z1));
+    const float x0 = (e0 < E) ? expf(z0 - m) : 0.f;
+    const float x1 = (e1 < E) ? expf(z1 - m) : 0.f;
+    const float s = group_sum<64>(x0 + x1);
+    v0 = round_bf16(x0 / s);
+    v1 = round_bf16(x1 / s);
+  }
+  const int kk = la ? a.kp : a.k;
+  bool sel0, sel1;
+  int r0, r1;
+  select_topk(e0 < E ? order_key(v0) : -1, e1 < E ? order_key(v1) : -1, kk, lane, sel0,
+              sel1, r0, r1);
+  if (la) {
+    if (sel0) a.pred[(int64_t)t * a.kp + r0] = e0;
+    if (sel1) a.pred[(int64_t)t * a.kp + r1] = e1;
+    return;
+  }
+  // scores of the selected experts
+  float sc0 = 0.f, sc1 = 0.f;
+  if (a.mode == MOE_ROUTE_SOFTMAX_TOPK) {
+    sc0 = v0;
+    sc1 = v1;
+    if (a.renorm) {
+      const float tot = round_bf16(group_sum<64>((sel0 ? v0 : 0.f) + (sel1 ? v1 : 0.f)));
+      sc0 = round_bf16(v0 / tot);
+      sc1 = round_bf16(v1 / tot);
+    }
+  } else {
+    const float m = wave_max(fmaxf(sel0 ? z0 : -INFINITY, sel1 ? z1 : -INFINITY));
+    const float x0 = sel0 ? expf(z0 - m) : 0.f;
+    const float x1 = sel1 ? expf(z1 - m) : 0.f;
+    const float s = group_sum<64>(x0 + x1);
+    sc0 = round_bf16(x0 / s);
+    sc1 = round_bf16(x1 / s);
+  }
+  bool miss0 = false, miss1 = false;
+  const int64_t o0 = (int64_t)t * a.k + r0, o1 = (int64_t)t * a.k + r1;
+  if (sel0) {
+    a.ids[o0] = e0;
+    a.scores[o0] = sc0;
+    if (a.table) {
+      const int32_t ref = a.table[e0];
+      a.slot_refs[o0] = ref;
+      miss0 = ref < 0;
+    }
+  }
+  if (sel1) {
+    a.ids[o1] = e1;
+    a.scores[o1] = sc1;
+    if (a.table) {
+      const int32_t ref = a.table[e1];
+      a.slot_refs[o1] = ref;
+      miss1 = ref < 0;
+    }
+  }
+  if (a.miss_count) {
+    const int m = popc64(__ballot(miss0)) + popc64(__ballot(miss1));
+    if (lane == 0 && m) atomicAdd(a.miss_count, m);
   }
 }
 
@@ -108,91 +198,55 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   __syncthreads();
   if (!s_last) return;
 
-  const int E = a.E;
   const int ntask = a.T * (a.Wn ? 2 : 1);
-  for (int task = wave; task < ntask; task += 4) {
-    const int t = task % a.T;
-    const bool la = task >= a.T;
-    const int e0 = lane, e1 = lane + 64;
-    const float *lg = a.logits + ((la ? 1 : 0) * a.T + t) * E;
-    const uint16_t *bias = la ? a.bias_n : a.bias;
-    float z0 = -INFINITY, z1 = -INFINITY;
-    if (e0 < E) {
-      float l = __hip_atomic_load(lg + e0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (bias) l += bf16_to_f32(bias[e0]);
-      z0 = round_bf16(l);
-    }
-    if (e1 < E) {
-      float l = __hip_atomic_load(lg + e1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (bias) l += bf16_to_f32(bias[e1]);
-      z1 = round_bf16(l);
-    }
-    // ranked quantity: bf16 softmax probabilities (SOFTMAX_TOPK router) or
-    // the bf16 logits (TOPK_SOFTMAX router, and every lookahead)
-    float v0 = z0, v1 = z1;
-    if (!la && a.mode == MOE_ROUTE_SOFTMAX_TOPK) {
-      const float m = wave_max(fmaxf(z0, z1));
-      const float x0 = (e0 < E) ? expf(z0 - m) : 0.f;
-      const float x1 = (e1 < E) ? expf(z1 - m) : 0.f;
-      const float s = group_sum<64>(x0 + x1);
-      v0 = round_bf16(x0 / s);
-      v1 = round_bf16(x1 / s);
-    }
-    const int kk = la ? a.kp : a.k;
-    bool sel0, sel1;
-    int r0, r1;
-    select_topk(e0 < E ? order_key(v0) : -1, e1 < E ? order_key(v1) : -1, kk, lane,
-                sel0, sel1, r0, r1);
-    if (la) {
-      if (sel0) a.pred[t * a.kp + r0] = e0;
-      if (sel1) a.pred[t * a.kp + r1] = e1;
-      continue;
-    }
-    // scores of the selected experts
-    float sc0 = 0.f, sc1 = 0.f;
-    if (a.mode == MOE_ROUTE_SOFTMAX_TOPK) {
-      sc0 = v0;
-      sc1 = v1;
-      if (a.renorm) {
-        const float tot = round_bf16(group_sum<64>((sel0 ? v0 : 0.f) + (sel1 ? v1 : 0.f)));
-        sc0 = round_bf16(v0 / tot);
-        sc1 = round_bf16(v1 / tot);
-      }
-    } else {
-      const float m = wave_max(fmaxf(sel0 ? z0 : -INFINITY, sel1 ? z1 : -INFINITY));
-      const float x0 = sel0 ? expf(z0 - m) : 0.f;
-      const float x1 = sel1 ? expf(z1 - m) : 0.f;
-      const float s = group_sum<64>(x0 + x1);
-      sc0 = round_bf16(x0 / s);
-      sc1 = round_bf16(x1 / s);
-    }
-    bool miss0 = false, miss1 = false;
-    if (sel0) {
-      a.ids[t * a.k + r0] = e0;
-      a.scores[t * a.k + r0] = sc0;
-      if (a.table) {
-        const int32_t ref = a.table[e0];
-        a.slot_refs[t * a.k + r0] = ref;
-        miss0 = ref < 0;
-      }
-    }
-    if (sel1) {
-      a.ids[t * a.k + r1] = e1;
-      a.scores[t * a.k + r1] = sc1;
-      if (a.table) {
-        const int32_t ref = a.table[e1];
-        a.slot_refs[t * a.k + r1] = ref;
-        miss1 = ref < 0;
-      }
-    }
-    if (a.miss_count) {
-      const int m = popc64(__ballot(miss0)) + popc64(__ballot(miss1));
-      if (lane == 0 && m) atomicAdd(a.miss_count, m);
-    }
-  }
+  for (int task = wave; task < ntask; task += 4) select_task(a, task, lane);
   __syncthreads();
   if (threadIdx.x == 0)
     __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// Many tokens (T > kRouteMaxT): the logits as a bf16 MFMA product.  One
+// workgroup = 16 tokens x 64 router rows, wave w = rows 16w..16w+15;
+// v_mfma_f32_16x16x32_bf16 with A = x rows (lane: row l%16, inputs
+// 8*(l/16)..+7 of each 32), B = router rows, fp32 accumulation.
+// blockIdx.y >= ceil(E/64) selects the lookahead router.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void route_logits_mfma_kernel(RouteArgs a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int eblocks = (a.E + 63) / 64;
+  const bool la = blockIdx.y >= eblocks;
+  const int t0 = blockIdx.x * 16, e0 = (blockIdx.y - (la ? eblocks : 0)) * 64 + wave * 16;
+  if (e0 >= a.E) return;
+  const int row = lane & 15, kq = lane >> 4;
+  const uint4 *xa =
+      reinterpret_cast<const uint4 *>(a.x + (int64_t)min(t0 + row, a.T - 1) * a.D);
+  const uint4 *wb = reinterpret_cast<const uint4 *>((la ? a.Wn : a.W) +
+                                                    (int64_t)min(e0 + row, a.E - 1) * a.D);
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  const int nk = a.D / 32;
+  for (int k = 0; k < nk; ++k) {
+    const uint4 xv = xa[k * 4 + kq], wv = wb[k * 4 + kq];
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xv),
+                                                  __builtin_bit_cast(bf16x8_t, wv), acc, 0,
+                                                  0, 0);
+  }
+  // result: lane holds router row e0 + l%16 for tokens t0 + 4*(l/16) + r
+  float *lg = a.logits + (int64_t)(la ? 1 : 0) * a.T * a.E;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = t0 + 4 * kq + r, e = e0 + row;
+    if (t < a.T && e < a.E) lg[(int64_t)t * a.E + e] = acc[r];
+  }
+}
+
+// one wave per selection task, after route_logits_mfma_kernel
+__global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
+  const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (task < a.T * (a.Wn ? 2 : 1)) select_task(a, task, threadIdx.x & 63);
 }
 
 __global__ void slot_lookup_kernel(const int32_t *table, int E,
@@ -212,6 +266,14 @@ __global__ void slot_lookup_kernel(const int32_t *table, int E,
 }
 
 void launch_route(const RouteArgs &a, hipStream_t s) {
+  if (a.T > kRouteMaxT) {
+    const int eblocks = (a.E + 63) / 64;
+    hipLaunchKernelGGL(route_logits_mfma_kernel, dim3((a.T + 15) / 16, eblocks * (a.Wn ? 2 : 1)),
+                       dim3(256), 0, s, a);
+    const int ntask = a.T * (a.Wn ? 2 : 1);
+    hipLaunchKernelGGL(route_select_kernel, dim3((ntask + 3) / 4), dim3(256), 0, s, a);
+    return;
+  }
   const int nrows = a.E * (a.Wn ? 2 : 1);
   const int nit = (a.D / 8 + 63) / 64;
   dim3 g((nrows + 3) / 4), b(256);

@@ -56,6 +56,36 @@ def ffn_decode(pool, slot_refs: torch.Tensor, scores: torch.Tensor,
 
     x bf16 [T, D]; slot_refs int32 [T, k]; scores fp32 [T, k].  Returns bf16
     [T, D] (and fills out_f32 when given)."""
+    return _ffn("moe_ffn_decode", "moe_ffn_decode_workspace", "ffn", pool, slot_refs,
+                scores, x, out, out_f32, stream, workspace)
+
+
+def ffn_grouped(pool, slot_refs: torch.Tensor, scores: torch.Tensor,
+                x: torch.Tensor, out: torch.Tensor | None = None,
+                out_f32: torch.Tensor | None = None, stream=None,
+                workspace: torch.Tensor | None = None):
+    """The expert block for many tokens (prefill): pairs grouped per slot,
+    bf16 MFMA per group.  Same arguments and result as ffn_decode."""
+    return _ffn("moe_ffn_grouped", "moe_ffn_grouped_workspace", "ffn_grouped", pool,
+                slot_refs, scores, x, out, out_f32, stream, workspace)
+
+
+# Above this many tokens per call the grouped MFMA path runs (each expert's
+# weights then serve several tokens per read); at or below it, the decode
+# kernels (one weight read per routed pair, no grouping pass).
+GROUPED_MIN_TOKENS = 16
+
+
+def ffn(pool, slot_refs, scores, x, out=None, out_f32=None, stream=None):
+    """The expert block, choosing the decode or the grouped path by T (the
+    decode/prefill split of engine_v3.py:555-600)."""
+    T = 1 if x.dim() == 1 else x.shape[0]
+    f = ffn_grouped if T > GROUPED_MIN_TOKENS else ffn_decode
+    return f(pool, slot_refs, scores, x, out, out_f32, stream)
+
+
+def _ffn(entry, ws_entry, ws_key, pool, slot_refs, scores, x, out, out_f32, stream,
+         workspace):
     geom: Geometry = pool.geom
     if x.dim() == 1:
         x = x.view(1, -1)
@@ -74,9 +104,11 @@ def ffn_decode(pool, slot_refs: torch.Tensor, scores: torch.Tensor,
         _req(out_f32, torch.float32, "out_f32", T * D, pool.device)
     g = geom.c_geom()
     L = _lib.lib()
-    need = L.moe_ffn_decode_workspace(C.byref(g), T, k)
-    ws = workspace if workspace is not None else _WS.get("ffn", need, x.device)
-    _lib.check(L.moe_ffn_decode(
+    need = getattr(L, ws_entry)(C.byref(g), T, k)
+    if need == 0:
+        raise ValueError(f"{entry}: unsupported T={T}, k={k}")
+    ws = workspace if workspace is not None else _WS.get(ws_key, need, x.device)
+    _lib.check(getattr(L, entry)(
         C.byref(pool.c_view()), C.byref(g), _p(slot_refs), _p(scores), _p(x),
         T, k, _p(out), _p(out_f32), _p(ws), ws.numel(), _lib.stream_ptr(stream)))
     return out if out is not None else out_f32

@@ -174,3 +174,61 @@ class DecodeStack:
         refs = torch.stack([b.slot_refs[0] for b in self.bufs]).cpu().numpy()
         pred = torch.stack([b.pred[0] for b in self.bufs]).cpu().numpy()
         return ids, sc, refs, pred
+
+
+class PrefillStack(DecodeStack):
+    """T tokens per layer through an n_layers stack (the batched/prefill
+    path): per layer, the many-token router (bf16 MFMA logits + top-k +
+    lookahead + slot lookup) and the grouped MFMA expert block, all on
+    device, no host round trip.  The pool, store, routers and residency are
+    those of DecodeStack."""
+
+    def __init__(self, geom: Geometry, n_layers: int, n_slots: int, n_tokens: int,
+                 device="cuda", **kw):
+        super().__init__(geom, n_layers, n_slots, device, **kw)
+        import ctypes as C
+        self.T = n_tokens
+        dev = self.device
+        self.bufs = [ops.RouteBuffers(n_tokens, self.k, self.k_pred, dev)
+                     for _ in range(n_layers)]
+        self.route_ws = torch.zeros(_lib.lib().moe_route_workspace(n_tokens, self.E),
+                                    dtype=torch.uint8, device=dev)
+        g = geom.c_geom()
+        self.ffn_ws = torch.zeros(
+            _lib.lib().moe_ffn_grouped_workspace(C.byref(g), n_tokens, self.k),
+            dtype=torch.uint8, device=dev)
+        self.x_in = torch.zeros((n_layers, n_tokens, geom.d_model), dtype=torch.bfloat16,
+                                device=dev)
+        self.y = torch.zeros((n_layers, n_tokens, geom.d_model), dtype=torch.bfloat16,
+                             device=dev)
+
+    def layer(self, Lx: int, stream=None):
+        g = self.geom
+        nxt = Lx + 1 < self.L
+        b = self.bias[Lx] if self.bias is not None else None
+        bn = self.bias[Lx + 1] if (self.bias is not None and nxt) else None
+        bufs = self.bufs[Lx]
+        ops.route(self.x_in[Lx], self.W[Lx], b, g.routing, g.norm_topk_prob, self.k,
+                  W_next=self.W[Lx + 1] if nxt else None, bias_next=bn,
+                  k_pred=self.k_pred, table=self.table[Lx], bufs=bufs,
+                  stream=stream, workspace=self.route_ws)
+        ops.ffn_grouped(self.pool, bufs.slot_refs, bufs.scores, self.x_in[Lx],
+                        out=self.y[Lx], stream=stream, workspace=self.ffn_ws)
+
+    def run_step(self, x_step: torch.Tensor, use_graph: bool = True):
+        """x_step: bf16 [n_layers, T, d_model], the residual stream of T tokens
+        at every layer."""
+        self.x_in.copy_(x_step, non_blocking=True)
+        if use_graph and self.graph is not None:
+            self.graph.replay()
+        else:
+            self.token_eager()
+
+    def pairs_per_layer(self) -> int:
+        return self.T * self.k
+
+    def routed_counts(self) -> np.ndarray:
+        """Per layer, the number of pairs routed to each expert (host copy)."""
+        ids = torch.stack([b.ids for b in self.bufs]).cpu().numpy()
+        return np.stack([np.bincount(ids[L].ravel(), minlength=self.E)
+                         for L in range(self.L)])

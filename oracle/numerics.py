@@ -19,6 +19,7 @@ Parity status (how each function is pinned, see tests/test_oracle_*.py):
                         case of the synthetic workloads.
   qmv / gather_qmm .... pinned: dense dequant-then-dot (np.einsum) and the
                         per-group factorisation of kernels.py:141-145 agree.
+  qmm / moe_block_batch pinned: row-by-row equal to qmv / moe_block.
   swiglu (Qwen3) ...... pinned: closed form silu(g)*u on special values.
   swiglu_clamped ...... pinned: saturation/clipping special cases.
   routers ............. pinned: brute-force full sort; invariants (distinct
@@ -110,6 +111,19 @@ def qmv(x, W, S_bits, B_bits, group: int = GROUP) -> np.ndarray:
     return (S * qx + B * xg.sum(-1)[None, :]).sum(-1)
 
 
+def qmm(X, W, S_bits, B_bits, group: int = GROUP) -> np.ndarray:
+    """The same product for many rows at once: Y = X @ deq(W).T, exact fp64
+    up to summation order (gather_qmm with transpose=True over [.., n, D]
+    inputs, engine_v3.py:588-598).  Dense dequant-then-product form."""
+    X = np.asarray(X, dtype=np.float64)
+    return X @ dequant(W, S_bits, B_bits, group).T
+
+
+def _qprod(x, W, S_bits, B_bits):
+    x = np.asarray(x, dtype=np.float64)
+    return qmv(x, W, S_bits, B_bits) if x.ndim == 1 else qmm(x, W, S_bits, B_bits)
+
+
 def _round(mode, v):
     return bf16r(v) if mode == "mlx" else np.asarray(v, dtype=np.float64)
 
@@ -163,10 +177,10 @@ def rank_desc(v) -> np.ndarray:
 def router_logits(x, W_bits, bias_bits=None, mode: str = "f64"):
     """Router linear layer x @ W.T (+ bias), bf16 weights [E, D].  MLX
     materialises a bf16 array, rounded once after the fused add
-    (nn.Linear -> addmm)."""
+    (nn.Linear -> addmm).  x is one token [D] or rows [T, D]."""
     x = np.asarray(x, dtype=np.float64)
     W = bf16_bits_to_f32(W_bits).astype(np.float64)
-    z = W @ x
+    z = x @ W.T
     if bias_bits is not None:
         z = z + bf16_bits_to_f32(bias_bits).astype(np.float64)
     return _round(mode, z)
@@ -238,14 +252,15 @@ def ids_match(ranked_on, ref_ids, got_ids, ulps: float = 1.0) -> bool:
 # --------------------------------------------------------------------------
 def expert_ffn_qwen3(x, e, mode: str = "f64"):
     """One expert of the Qwen3 block.  `e` is a dict of per-expert arrays:
-    gate/up/down .weight (u32), .scales/.biases (bf16 bits)."""
-    up = _round(mode, qmv(x, e["up_proj.weight"], e["up_proj.scales"],
-                          e["up_proj.biases"]))
-    gate = _round(mode, qmv(x, e["gate_proj.weight"], e["gate_proj.scales"],
-                            e["gate_proj.biases"]))
+    gate/up/down .weight (u32), .scales/.biases (bf16 bits).  x is one
+    token [D] or a batch of rows [n, D]."""
+    up = _round(mode, _qprod(x, e["up_proj.weight"], e["up_proj.scales"],
+                             e["up_proj.biases"]))
+    gate = _round(mode, _qprod(x, e["gate_proj.weight"], e["gate_proj.scales"],
+                               e["gate_proj.biases"]))
     h = swiglu(gate, up, mode)
-    y = _round(mode, qmv(h, e["down_proj.weight"], e["down_proj.scales"],
-                         e["down_proj.biases"]))
+    y = _round(mode, _qprod(h, e["down_proj.weight"], e["down_proj.scales"],
+                            e["down_proj.biases"]))
     return y
 
 
@@ -253,8 +268,8 @@ def expert_ffn_gptoss(x, e, alpha=1.702, limit=7.0, mode: str = "f64"):
     """One expert of the gpt-oss block: each projection adds its bias vector
     after the quantised product (engine_120b.py:136-139)."""
     def proj(name, inp):
-        y = _round(mode, qmv(inp, e[f"{name}.weight"], e[f"{name}.scales"],
-                             e[f"{name}.biases"]))
+        y = _round(mode, _qprod(inp, e[f"{name}.weight"], e[f"{name}.scales"],
+                                e[f"{name}.biases"]))
         return _round(mode, y + bf16_bits_to_f32(e[f"{name}.bias"]))
     up = proj("up_proj", x)
     gate = proj("gate_proj", x)
@@ -279,6 +294,31 @@ def moe_block(x, experts, scores, kind: str = "qwen3", mode: str = "f64",
     else:
         ys = [expert_ffn_gptoss(x, e, alpha, limit, mode) for e in experts]
     return combine(ys, scores, mode)
+
+
+def moe_block_batch(X, ids, scores, expert, kind: str = "qwen3", mode: str = "f64",
+                    alpha=1.702, limit=7.0):
+    """The expert block for T tokens: X [T, D], ids/scores [T, k], expert(e)
+    -> per-expert dict.  Each expert runs once over all rows routed to it
+    (the batched gather_qmm of the prefill path, engine_v3.py:588-600);
+    then per token the score-weighted sum over ranks in rank order."""
+    X = np.asarray(X, dtype=np.float64)
+    ids = np.asarray(ids)
+    T, k = ids.shape
+    Y = None
+    for e in np.unique(ids):
+        t, r = np.nonzero(ids == e)
+        ex = expert(int(e))
+        if kind == "qwen3":
+            ye = expert_ffn_qwen3(X[t], ex, mode)
+        else:
+            ye = expert_ffn_gptoss(X[t], ex, alpha, limit, mode)
+        if Y is None:
+            Y = np.zeros((T, k, ye.shape[-1]))
+        Y[t, r] = ye
+    s = np.asarray(scores, dtype=np.float64)
+    prod = _round(mode, Y * s[:, :, None])
+    return _round(mode, prod.sum(1))
 
 
 def rel_err(a, b) -> float:

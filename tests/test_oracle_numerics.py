@@ -237,6 +237,46 @@ def test_block_dense_reference_gptoss_bias_and_clamp():
     np.testing.assert_allclose(y, ref, rtol=1e-10, atol=1e-12)
 
 
+def test_qmm_rows_equal_qmv():
+    rng = np.random.default_rng(11)
+    W, S, B = _rand_expert_row(rng, 24, 192)
+    X = rng.normal(size=(5, 192))
+    Y = N.qmm(X, W, S, B)
+    assert Y.shape == (5, 24)
+    for t in range(5):
+        np.testing.assert_allclose(Y[t], N.qmv(X[t], W, S, B), rtol=1e-12, atol=1e-14)
+
+
+def test_router_logits_rows_equal_single_token():
+    rng = np.random.default_rng(12)
+    W = N.f32_to_bf16_bits(rng.normal(0, 0.02, (16, 64)))
+    b = N.f32_to_bf16_bits(rng.normal(0, 0.1, 16))
+    X = rng.normal(size=(3, 64))
+    Z = N.router_logits(X, W, b)
+    for t in range(3):
+        np.testing.assert_allclose(Z[t], N.router_logits(X[t], W, b), rtol=1e-13)
+
+
+@pytest.mark.parametrize("kind", ["qwen3", "gptoss"])
+def test_block_batch_equals_per_token(kind):
+    """The grouped (per-expert batched) restatement equals the per-token
+    block on every token, with experts repeating across tokens."""
+    rng = np.random.default_rng(13)
+    D, F, E, T, k = 128, 64, 6, 9, 3
+    exps = [_expert(rng, D, F, bias=(kind == "gptoss")) for _ in range(E)]
+    X = rng.normal(size=(T, D))
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)])
+    sc = rng.dirichlet(np.ones(k), T)
+    for mode in ("f64", "mlx"):
+        Y = N.moe_block_batch(X, ids, sc, lambda e: exps[e], kind, mode)
+        for t in range(T):
+            y = N.moe_block(X[t], [exps[e] for e in ids[t]], sc[t], kind, mode)
+            if mode == "f64":
+                np.testing.assert_allclose(Y[t], y, rtol=1e-10, atol=1e-12)
+            else:   # bf16 rounding points may flip by one ulp on a sum-order change
+                assert N.rel_err(Y[t], y) < 2 ** -6
+
+
 def test_combine_permutation_invariant_and_linear():
     rng = np.random.default_rng(9)
     ys = rng.normal(size=(8, 16))
