@@ -207,39 +207,58 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
 
 // ---------------------------------------------------------------------------
 // Many tokens (T > kRouteMaxT): the logits as a bf16 MFMA product.  One
-// workgroup = 16 tokens x 64 router rows, wave w = rows 16w..16w+15;
-// v_mfma_f32_16x16x32_bf16 with A = x rows (lane: row l%16, inputs
-// 8*(l/16)..+7 of each 32), B = router rows, fp32 accumulation.
-// blockIdx.y >= ceil(E/64) selects the lookahead router.
+// workgroup = 16 tokens x 16 router rows; its 4 waves take interleaved
+// 32-input steps of K (v_mfma_f32_16x16x32_bf16: A = x rows, lane row l%16,
+// inputs 8*(l/16)..+7 of the step; B = router rows) and the four fp32
+// partial products are summed in a fixed order through LDS.
+// blockIdx.y >= ceil(E/16) selects the lookahead router.
 // ---------------------------------------------------------------------------
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(256) void route_logits_mfma_kernel(RouteArgs a) {
+  __shared__ float part[4][16][17];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int eblocks = (a.E + 63) / 64;
+  const int eblocks = (a.E + 15) / 16;
   const bool la = blockIdx.y >= eblocks;
-  const int t0 = blockIdx.x * 16, e0 = (blockIdx.y - (la ? eblocks : 0)) * 64 + wave * 16;
-  if (e0 >= a.E) return;
+  const int t0 = blockIdx.x * 16, e0 = (blockIdx.y - (la ? eblocks : 0)) * 16;
   const int row = lane & 15, kq = lane >> 4;
   const uint4 *xa =
-      reinterpret_cast<const uint4 *>(a.x + (int64_t)min(t0 + row, a.T - 1) * a.D);
+      reinterpret_cast<const uint4 *>(a.x + (int64_t)min(t0 + row, a.T - 1) * a.D) + kq;
   const uint4 *wb = reinterpret_cast<const uint4 *>((la ? a.Wn : a.W) +
-                                                    (int64_t)min(e0 + row, a.E - 1) * a.D);
+                                                    (int64_t)min(e0 + row, a.E - 1) * a.D) + kq;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   const int nk = a.D / 32;
-  for (int k = 0; k < nk; ++k) {
-    const uint4 xv = xa[k * 4 + kq], wv = wb[k * 4 + kq];
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xv),
-                                                  __builtin_bit_cast(bf16x8_t, wv), acc, 0,
-                                                  0, 0);
-  }
-  // result: lane holds router row e0 + l%16 for tokens t0 + 4*(l/16) + r
-  float *lg = a.logits + (int64_t)(la ? 1 : 0) * a.T * a.E;
+  int k = wave;
+  for (; k + 12 < nk; k += 16) {   // four steps per iteration, loads first
+    uint4 xv[4], wv[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int t = t0 + 4 * kq + r, e = e0 + row;
-    if (t < a.T && e < a.E) lg[(int64_t)t * a.E + e] = acc[r];
+    for (int u = 0; u < 4; ++u) {
+      xv[u] = xa[(k + 4 * u) * 4];
+      wv[u] = wb[(k + 4 * u) * 4];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xv[u]),
+                                                    __builtin_bit_cast(bf16x8_t, wv[u]), acc,
+                                                    0, 0, 0);
+  }
+  for (; k < nk; k += 4)
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, xa[k * 4]),
+                                                  __builtin_bit_cast(bf16x8_t, wb[k * 4]), acc,
+                                                  0, 0, 0);
+  // lane holds router row e0 + l%16 for tokens t0 + 4*(l/16) + r
+#pragma unroll
+  for (int r = 0; r < 4; ++r) part[wave][4 * kq + r][row] = acc[r];
+  __syncthreads();
+  if (wave == 0) {
+    float *lg = a.logits + (int64_t)(la ? 1 : 0) * a.T * a.E;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tt = 4 * kq + r, t = t0 + tt, e = e0 + row;
+      const float v = (part[0][tt][row] + part[1][tt][row]) + (part[2][tt][row] + part[3][tt][row]);
+      if (t < a.T && e < a.E) lg[(int64_t)t * a.E + e] = v;
+    }
   }
 }
 
@@ -267,7 +286,7 @@ __global__ void slot_lookup_kernel(const int32_t *table, int E,
 
 void launch_route(const RouteArgs &a, hipStream_t s) {
   if (a.T > kRouteMaxT) {
-    const int eblocks = (a.E + 63) / 64;
+    const int eblocks = (a.E + 15) / 16;
     hipLaunchKernelGGL(route_logits_mfma_kernel, dim3((a.T + 15) / 16, eblocks * (a.Wn ? 2 : 1)),
                        dim3(256), 0, s, a);
     const int ntask = a.T * (a.Wn ? 2 : 1);
