@@ -24,6 +24,21 @@ from .geometry import Geometry
 from .pool import SlotPool, _norm_device
 
 
+def routers(geom: Geometry, n_layers: int, device, seed: int, zipf_s: float | None,
+            router_bias: bool):
+    """Router weights [L, E, D] and bias [L, E] (or None) of the synthetic
+    stacks: bf16 N(0, 0.02) weights, optional bf16 N(0, 0.02) bias, plus a
+    Zipf(zipf_s) log-popularity per layer on the logits.  Returns (W, bias,
+    log-popularity or None)."""
+    W, b = synth.router_weights(geom, n_layers, device, seed + 1, with_bias=router_bias)
+    logpop = None
+    if zipf_s is not None:
+        logpop = synth.zipf_log_popularity(n_layers, geom.n_experts, zipf_s, seed + 2)
+        zb = synth.bf16_bias_from_log(logpop, device)
+        b = zb if b is None else (b.float() + zb.float()).to(torch.bfloat16)
+    return W, b, logpop
+
+
 class DecodeStack:
     def __init__(self, geom: Geometry, n_layers: int, n_slots: int, device="cuda",
                  seed: int = synth.SEED_BASE + 2, zipf_s: float | None = 1.1,
@@ -38,15 +53,8 @@ class DecodeStack:
         n_rec = n_layers * self.E
         self.store = synth.make_store(geom, n_rec, self.device, seed)
         self.pool = SlotPool(geom, n_slots, self.device, store=self.store)
-        W, b = synth.router_weights(geom, n_layers, self.device, seed + 1,
-                                    with_bias=router_bias)
-        self.W = W
-        self.logpop = None
-        if zipf_s is not None:
-            self.logpop = synth.zipf_log_popularity(n_layers, self.E, zipf_s, seed + 2)
-            zb = synth.bf16_bias_from_log(self.logpop, self.device)
-            b = zb if b is None else (b.float() + zb.float()).to(torch.bfloat16)
-        self.bias = b
+        self.W, self.bias, self.logpop = routers(geom, n_layers, self.device, seed,
+                                                 zipf_s, router_bias)
         # residency: `resident` (layer, expert) pairs in the pool, in a seeded
         # random slot placement; the rest read from the store
         if resident is None:
@@ -232,3 +240,48 @@ class PrefillStack(DecodeStack):
         ids = torch.stack([b.ids for b in self.bufs]).cpu().numpy()
         return np.stack([np.bincount(ids[L].ravel(), minlength=self.E)
                          for L in range(self.L)])
+
+
+class StreamingStack:
+    """The reference's engine loop over a pool smaller than the model: per
+    layer, streaming_call (route + lookahead, one host synchronisation,
+    prefetch of the predicted layer-L+1 experts, acquire, the expert block;
+    engine_v3.py:493-609) on an ExpertPool whose fills come from a pinned
+    host store by hipMemcpyAsync, prefetches on a side stream.  Store
+    records, routers and inputs are those of DecodeStack with the same seed,
+    so the two produce identical outputs."""
+
+    def __init__(self, geom: Geometry, n_layers: int, n_slots: int, device="cuda",
+                 seed: int = synth.SEED_BASE + 2, zipf_s: float | None = 1.1,
+                 router_bias: bool = False, widen: int = 1, host_store=None,
+                 evict: str | None = None):
+        from .block import MoEBlock
+        from .pool import ExpertPool
+        self.geom = geom
+        self.L = n_layers
+        self.E = geom.n_experts
+        self.k = geom.top_k
+        self.device = _norm_device(device)
+        self.store = host_store if host_store is not None else \
+            synth.make_host_store(geom, n_layers * self.E, self.device, seed)
+        self.pool = ExpertPool(geom, n_slots, self.store, self.device, evict=evict,
+                               widen=widen, n_layers=n_layers)
+        self.W, self.bias, self.logpop = routers(geom, n_layers, self.device, seed,
+                                                 zipf_s, router_bias)
+        self.blocks = []
+        for Lx in range(n_layers):
+            self.blocks.append(MoEBlock(Lx, geom, self.pool, self.W[Lx],
+                                        None if self.bias is None else self.bias[Lx],
+                                        self.blocks, widen=widen))
+
+    def token(self, x_tok: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+        """x_tok: bf16 [n_layers, d_model]; returns y bf16 [n_layers, d_model]."""
+        if out is None:
+            out = torch.empty_like(x_tok)
+        for Lx, blk in enumerate(self.blocks):
+            out[Lx:Lx + 1] = blk(x_tok[Lx:Lx + 1])
+        return out
+
+    def recall(self) -> float:
+        r = [v for b in self.blocks for v in b.recall]
+        return float(np.mean(r)) if r else float("nan")

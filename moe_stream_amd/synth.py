@@ -38,23 +38,25 @@ def fill_records(store: torch.Tensor, geom: Geometry, gen: torch.Generator,
     """Write synthetic expert weights into every record of `store`."""
     n = store.shape[0]
     chunk = max(1, chunk_bytes // geom.record_bytes)
-    dev = store.device
     for lo in range(0, n, chunk):
-        hi = min(n, lo + chunk)
-        part = store[lo:hi]
-        for p in ("gate_proj", "up_proj", "down_proj"):
-            w = comp_view(part, geom, f"{p}.weight")
-            w.copy_(torch.randint(-2**31, 2**31, w.shape, dtype=torch.int64,
-                                  generator=gen, device=dev).to(torch.int32))
-            s = comp_view(part, geom, f"{p}.scales")
-            sv = (torch.randn(s.shape, generator=gen, device=dev) * 0.02).abs()
-            s.copy_(sv.to(torch.bfloat16))
-            b = comp_view(part, geom, f"{p}.biases")
-            b.copy_((s.float() * -8.0).to(torch.bfloat16))   # exact: power of 2
-            if geom.has_proj_bias:
-                pb = comp_view(part, geom, f"{p}.bias")
-                pb.copy_((torch.randn(pb.shape, generator=gen, device=dev) * 0.02
-                          ).to(torch.bfloat16))
+        _fill_chunk(store[lo:min(n, lo + chunk)], geom, gen)
+
+
+def _fill_chunk(part: torch.Tensor, geom: Geometry, gen: torch.Generator) -> None:
+    dev = part.device
+    for p in ("gate_proj", "up_proj", "down_proj"):
+        w = comp_view(part, geom, f"{p}.weight")
+        w.copy_(torch.randint(-2**31, 2**31, w.shape, dtype=torch.int64,
+                              generator=gen, device=dev).to(torch.int32))
+        s = comp_view(part, geom, f"{p}.scales")
+        sv = (torch.randn(s.shape, generator=gen, device=dev) * 0.02).abs()
+        s.copy_(sv.to(torch.bfloat16))
+        b = comp_view(part, geom, f"{p}.biases")
+        b.copy_((s.float() * -8.0).to(torch.bfloat16))   # exact: power of 2
+        if geom.has_proj_bias:
+            pb = comp_view(part, geom, f"{p}.bias")
+            pb.copy_((torch.randn(pb.shape, generator=gen, device=dev) * 0.02
+                      ).to(torch.bfloat16))
 
 
 def make_store(geom: Geometry, n_records: int, device, seed: int) -> torch.Tensor:
@@ -62,6 +64,26 @@ def make_store(geom: Geometry, n_records: int, device, seed: int) -> torch.Tenso
                         device=device)
     fill_records(store, geom, generator(device, seed))
     return store
+
+
+def make_host_store(geom: Geometry, n_records: int, device, seed: int,
+                    chunk_bytes: int = 256 << 20):
+    """The records of make_store(geom, n_records, device, seed), byte for
+    byte, in a pinned host store: generated chunk by chunk on `device` with
+    the same generator sequence and copied down."""
+    from .pool import HostStore
+    hs = HostStore(geom, n_records)
+    gen = generator(device, seed)
+    chunk = max(1, chunk_bytes // geom.record_bytes)
+    buf = torch.zeros((chunk, geom.record_bytes), dtype=torch.uint8, device=device)
+    for lo in range(0, n_records, chunk):
+        hi = min(n_records, lo + chunk)
+        part = buf[:hi - lo]
+        part.zero_()
+        _fill_chunk(part, geom, gen)
+        torch.from_numpy(hs.array[lo:hi]).copy_(part.cpu())
+    del buf
+    return hs
 
 
 def router_weights(geom: Geometry, n_layers: int, device, seed: int,
