@@ -336,7 +336,7 @@ size_t moe_stack_workspace(const moe_geom *g, int32_t n_layers, int32_t E, int32
   if (!g || n_layers <= 0 || E <= 0 || k <= 0) return 0;
   const size_t counters = (size_t)n_layers * moe::kCountersPerLayer * moe::kCounterWords * 4;
   const size_t logits = ((size_t)2 * E * 4 + 255) & ~(size_t)255;
-  const size_t h = ((size_t)k * g->d_ff * 4 + 255) & ~(size_t)255;
+  const size_t h = ((size_t)2 * k * g->d_ff * 2 + 255) & ~(size_t)255;   // bf16: predicted, fix-up
   return counters + logits + h;
 }
 
@@ -390,7 +390,7 @@ int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_lay
   ws += (size_t)n_layers * moe::kCountersPerLayer * moe::kCounterWords * 4;
   a.logits = reinterpret_cast<float *>(ws);
   ws += ((size_t)2 * E * 4 + 255) & ~(size_t)255;
-  a.h = reinterpret_cast<float *>(ws);
+  a.h = reinterpret_cast<uint16_t *>(ws);
   a.L = n_layers;
   a.E = E;
   a.kp = k_pred;

@@ -4,24 +4,35 @@
 // cost ~2.5 us each of launch overhead on this part, more than the 21 MB a
 // layer reads takes to stream.  Here a persistent grid of one workgroup per
 // CU walks all layers; the phases of a layer are chained by device-scope
-// counters (release on arrival, acquire on wait) instead of kernel
-// boundaries:
+// counters (a relaxed increment after the producer's stores completed;
+// device-scope loads on the consumer side) instead of kernel boundaries.
 //
-//   R_l : router (+ next-layer lookahead) rows, one row per workgroup;
-//         waits for D_{l-1} (the layer input depends on the previous output)
-//   -   : every workgroup waits for R_l, then ranks the logits itself
-//         (redundantly, identically) -- no extra hop to publish the choice
-//   U_l : gate/up + activation, 24 rows of one routed expert per workgroup;
-//         the workgroup's down-projection codes for phase D are issued to
-//         the memory system before this phase's math
-//   D_l : waits for U_l; down + score-weighted combine over the k experts,
-//         8 output rows per workgroup
+// The lookahead router predicts layer l+1's experts during layer l
+// (engine_v3.py:509-527).  Here that prediction stages the expert bytes:
+// at the end of layer l every workgroup issues the register loads of the
+// gate/up and down codes it will need in layer l+1 if the prediction is
+// right, so the reads overlap the wait for the layer boundary.  Per layer:
+//
+//   wait   : layer l-1 complete (its output is this layer's input)
+//   split  : waves 0-5 gate/up + activation for the PREDICTED expert at this
+//            workgroup's position (24 rows); wave 6 one router row (+ the
+//            lookahead row), then the lookahead ranking of layer l+1; wave 7
+//            waits for all router rows and ranks them (every workgroup
+//            redundantly, identically)
+//   fix-up : routed experts that were not predicted get gate/up now
+//   D      : down + score-weighted combine over the k routed experts, 8
+//            output rows per workgroup, wave = expert; then the staging
+//            loads of layer l+1
+//
+// Activations and the combine are indexed by routing rank, so results are
+// bit-identical to route_kernel + ffn_decode whatever was predicted.
 //
 // Counters are monotonic across launches: launch number `epoch` (1, 2, ...)
-// waits for epoch * arrivals, so the workspace is zeroed once.  Every wait is
-// bounded: past the spin limit it sets the device error word and proceeds
-// (wrong results, never a hang).  The cooperative launch guarantees that all
-// workgroups are resident, so every wait is satisfiable.
+// waits for epoch * arrivals, so the workspace is zeroed once; every counter
+// receives its full count of arrivals in every layer, work or not.  Every
+// wait is bounded: past the spin limit it sets the device error word and
+// proceeds (wrong results, never a hang).  The cooperative launch guarantees
+// that all workgroups are resident, so every wait is satisfiable.
 //
 // Semantics per layer are those of route_kernel + ffn_decode (see their
 // files): top_k_experts / top_k_route (engine_v3.py:467-473,
@@ -46,7 +57,7 @@ struct StackArgs {
   int32_t *pred;          // [L][KP]
   int32_t *miss;          // [L]
   float *logits;          // ws [2][E]
-  float *h;               // ws [K][F] bf16-valued floats
+  uint16_t *h;            // ws [2][K][F] bf16 activations: predicted, fix-up
   uint32_t *cnt;          // ws [L][3][kSub] counters, 128 B apart
   int L, E, kp, mode, renorm, act;
   float alpha, limit;
@@ -59,16 +70,17 @@ struct StackArgs {
 constexpr int kTraceWGs = 8;
 constexpr int kTracePoints = 12;
 enum { TR_START, TR_R_WAITED, TR_R_ARRIVED, TR_SELECTED, TR_U_ARRIVED,
-       TR_D_WAITED, TR_D_ARRIVED, TR_R_ALL, TR_LOGITS, TR_SOFTMAX, TR_TOPK };
+       TR_D_WAITED, TR_D_ARRIVED, TR_R_ALL, TR_LOGITS, TR_SOFTMAX, TR_TOPK, TR_FIXED };
 
+// Called by one wave at a time; its lane 0 stamps.
 __device__ __forceinline__ void trace_mark(const StackArgs &a, int l, int point) {
-  if (a.trace && blockIdx.x < kTraceWGs && threadIdx.x == 0)
+  if (a.trace && blockIdx.x < kTraceWGs && (threadIdx.x & 63) == 0)
     a.trace[((size_t)blockIdx.x * a.L + l) * kTracePoints + point] = wall_clock64();
 }
 // Stamp once `dep` has been computed (keeps the clock read after its inputs).
 __device__ __forceinline__ void trace_mark_after(const StackArgs &a, int l, int point,
                                                  float dep) {
-  if (a.trace && blockIdx.x < kTraceWGs && threadIdx.x == 0) {
+  if (a.trace && blockIdx.x < kTraceWGs && (threadIdx.x & 63) == 0) {
     __builtin_amdgcn_s_waitcnt(0);
     uint64_t t = wall_clock64();
     if (dep == 1.2345e-37f) t = 0;   // data dependence only
@@ -81,13 +93,25 @@ __device__ __forceinline__ void trace_mark_after(const StackArgs &a, int l, int 
 constexpr int kSub = 8;
 constexpr int kCounterWords = kSub * 32;
 
-// Counters of one layer: router rows, lookahead rows, the layer output, and
-// one per routed expert for its activations h.
-enum { CNT_R = 0, CNT_RL = 1, CNT_D = 2, CNT_U0 = 3 };
-constexpr int kCountersPerLayer = CNT_U0 + 8;
+// Counters of one layer: router rows, lookahead rows, the layer output, one
+// per predicted position for its activations, one per fix-up slot.
+enum { CNT_R = 0, CNT_RL = 1, CNT_D = 2, CNT_U0 = 3, CNT_F0 = 11 };
+constexpr int kCountersPerLayer = CNT_F0 + 8;
 
 __device__ __forceinline__ uint32_t *counter(const StackArgs &a, int l, int which) {
   return a.cnt + ((size_t)l * kCountersPerLayer + which) * kCounterWords;
+}
+
+// Two 16-byte device-scope (sc1) loads, waited for together.
+__device__ __forceinline__ void ld_dev_b128x2(const void *p0, const void *p1, uint4 &v0,
+                                              uint4 &v1) {
+  asm volatile(
+      "global_load_dwordx4 %0, %2, off sc1\n"
+      "global_load_dwordx4 %1, %3, off sc1\n"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(v0), "=&v"(v1)
+      : "v"(p0), "v"(p1)
+      : "memory");
 }
 
 // 16 bytes at device scope (4 x sc1 dword loads issued back to back).
@@ -146,6 +170,15 @@ __device__ __forceinline__ void wg_wait(const uint32_t *c, uint32_t target) {
   __syncthreads();
 }
 
+// One whole wave, after its own global stores: one arrival (phases in which
+// only this wave stores).
+__device__ __forceinline__ void wave_arrive(uint32_t *c) {
+  __builtin_amdgcn_s_waitcnt(0);
+  if ((threadIdx.x & 63) == 0)
+    __hip_atomic_fetch_add(c + (blockIdx.x % kSub) * 32, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // All threads of the workgroup, after their global stores: one arrival.
 // Every thread waits for its own stores to complete before the barrier, so
 // the relaxed increment is ordered after all of them.
@@ -159,6 +192,8 @@ __device__ __forceinline__ void wg_arrive(uint32_t *c) {
 
 template <int D, int F, int K, bool PBIAS>
 struct StackCfg {
+  static constexpr int D_ = D, F_ = F, K_ = K;
+  static constexpr bool PBIAS_ = PBIAS;
   static constexpr int NT = 512;                 // 8 waves
   // gate/up: SG 16 lanes per row, 4 rows per wave step, 6 waves -> 24 rows
   static constexpr int U = D / 32, NG = D / 64;
@@ -173,21 +208,144 @@ struct StackCfg {
   static constexpr int ITEMS_D = D / ROWS_D;
   static constexpr int SBD_U4 = ROWS_D * NGF * 2 / 16;
   static constexpr int NP = PBIAS ? 4 : 3;
+  static constexpr int SIT = (4 * SB_U4 + NT - 1) / NT;   // gate/up scale pieces per thread
+  static constexpr int SDIT = (2 * SBD_U4 + 63) / 64;     // down scale pieces per lane
   static_assert(U % SGU == 0, "gate/up rows split evenly over lanes");
   static_assert(F % ROWS_U == 0 && D % ROWS_D == 0, "row blocks");
   static_assert(K <= 8, "one wave per expert in the down phase");
   static_assert((ROWS_U * NG * 2) % 16 == 0 && (ROWS_D * NGF * 2) % 16 == 0, "scale blocks");
 };
 
+// Gate/up rows of one expert for this workgroup's 24-row block, waves
+// 0..WAVES_U-1: codes in cg/cu, scales staged in sbu_l, x staged in act_l
+// and asum_l.  Writes the bf16-rounded activations to hdst[row] (device
+// scope); ref < 0 past the store flags an error and writes zeros.
+template <class C>
+__device__ __forceinline__ void u_rows(const StackArgs &a, int32_t ref, int row0,
+                                       const uint4 (&cg)[C::CPLU], const uint4 (&cu)[C::CPLU],
+                                       const uint4 *act_l, const float *asum_l,
+                                       const uint4 (*sbu_l)[C::SB_U4], uint16_t *hdst) {
+  constexpr int U = C::U, NG = C::NG, SGU = C::SGU, CPLU = C::CPLU, RPSU = C::RPSU;
+  constexpr int SB_U4 = C::SB_U4, NP = C::NP;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int uj = lane % SGU, usub = lane / SGU;
+  const bool ok = resolve(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref) != nullptr;
+  const int urow = row0 + wave * RPSU + usub;
+  float pg = 0.f, pu = 0.f;
+  if (ok) {
+    const uint16_t *sbh = reinterpret_cast<const uint16_t *>(&sbu_l[0][0]);
+    constexpr int SBN = SB_U4 * 8;
+    const int rl = wave * RPSU + usub;
+#pragma unroll
+    for (int i = 0; i < CPLU; ++i) {
+      const int c = i * SGU + uj;
+      const int g = rl * NG + (c >> 1);
+      const float Sg = bf16_to_f32(sbh[g]), Bg = bf16_to_f32(sbh[SBN + g]);
+      const float Su = bf16_to_f32(sbh[2 * SBN + g]), Bu = bf16_to_f32(sbh[3 * SBN + g]);
+      const float xs = asum_l[c];
+      pg += Sg * chunk_dot_lds<U>(cg[i], act_l, c) + (Bg - 128.f * Sg) * xs;
+      pu += Su * chunk_dot_lds<U>(cu[i], act_l, c) + (Bu - 128.f * Su) * xs;
+    }
+  }
+  pg = group_sum<SGU>(pg);
+  pu = group_sum<SGU>(pu);
+  // every lane of a 16-lane row group holds that row's sums
+  uint32_t hb = 0;
+  if (ok) {
+    if (C::PBIAS_) {
+      pg += bf16_to_f32(reinterpret_cast<const uint16_t *>(
+          resolve(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref))[urow]);
+      pu += bf16_to_f32(reinterpret_cast<const uint16_t *>(
+          resolve(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref))[urow]);
+    }
+    hb = f32_to_bf16(apply_act(a.act, pg, pu, a.alpha, a.limit));
+  } else if (lane == 0) {
+    flag_error();
+  }
+  // the wave's RPSU = 4 consecutive rows as one 8-byte device-scope store
+  static_assert(RPSU == 4, "four rows per wave");
+  const uint32_t h0 = __builtin_amdgcn_readlane(hb, 0), h1 = __builtin_amdgcn_readlane(hb, 16);
+  const uint32_t h2 = __builtin_amdgcn_readlane(hb, 32), h3 = __builtin_amdgcn_readlane(hb, 48);
+  if (lane == 0) {
+    const uint64_t v = (uint64_t)(h0 | (h1 << 16)) | ((uint64_t)(h2 | (h3 << 16)) << 32);
+    __hip_atomic_store(reinterpret_cast<uint64_t *>(hdst + row0 + wave * RPSU), v,
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Register loads of one workgroup's gate/up block (waves 0..WAVES_U-1: the
+// codes of its rows; every thread: its share of the block's scales).
+template <class C>
+__device__ __forceinline__ void u_load(const StackArgs &a, int32_t ref, int row0,
+                                       uint4 (&cg)[C::CPLU], uint4 (&cu)[C::CPLU],
+                                       uint4 (&sr)[C::SIT]) {
+  constexpr int D = C::D_, NG = C::NG, SGU = C::SGU, CPLU = C::CPLU, RPSU = C::RPSU;
+  constexpr int SB_U4 = C::SB_U4, NP = C::NP, NT = C::NT;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const char *gw = resolve(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref);
+  if (gw == nullptr) return;
+  const char *uw = resolve(a.pa, comp_index(PROJ_UP, PART_W, NP), ref);
+#pragma unroll
+  for (int it = 0; it < C::SIT; ++it) {
+    const int i = it * NT + tid;
+    const int p = i / SB_U4, o = i % SB_U4;
+    const int part = (p & 1) ? PART_B : PART_S, proj = (p >> 1) ? PROJ_UP : PROJ_GATE;
+    const char *sp = resolve(a.pa, comp_index(proj, part, NP), ref);
+    sr[it] = (i < 4 * SB_U4) ? reinterpret_cast<const uint4 *>(sp + (int64_t)row0 * NG * 2)[o]
+                             : make_uint4(0, 0, 0, 0);
+  }
+  if (wave < C::WAVES_U) {
+    const int uj = lane % SGU, usub = lane / SGU;
+    const int urow = row0 + wave * RPSU + usub;
+    const uint4 *g4 = reinterpret_cast<const uint4 *>(gw + (int64_t)urow * (D / 2));
+    const uint4 *u4 = reinterpret_cast<const uint4 *>(uw + (int64_t)urow * (D / 2));
+#pragma unroll
+    for (int i = 0; i < CPLU; ++i) {
+      cg[i] = load_stream16(g4 + i * SGU + uj);
+      cu[i] = load_stream16(u4 + i * SGU + uj);
+    }
+  }
+}
+
+// Register loads of one wave's down rows (8 output rows) of one expert.
+template <class C>
+__device__ __forceinline__ void d_load(const StackArgs &a, int32_t ref, int drow0,
+                                       uint4 (&cd)[C::CPLD], uint4 (&sdr)[C::SDIT]) {
+  constexpr int F = C::F_, NGF = C::NGF, SGD = C::SGD, CPLD = C::CPLD, UF = C::UF;
+  constexpr int SBD_U4 = C::SBD_U4, NP = C::NP;
+  const int lane = threadIdx.x & 63;
+  const char *dw = resolve(a.pa, comp_index(PROJ_DOWN, PART_W, NP), ref);
+  if (dw == nullptr) return;
+#pragma unroll
+  for (int it = 0; it < C::SDIT; ++it) {
+    const int i = it * 64 + lane;
+    const int p = i / SBD_U4, o = i % SBD_U4;
+    const char *sp = resolve(a.pa, comp_index(PROJ_DOWN, p ? PART_B : PART_S, NP), ref);
+    sdr[it] = (i < 2 * SBD_U4) ? reinterpret_cast<const uint4 *>(sp + (int64_t)drow0 * NGF * 2)[o]
+                               : make_uint4(0, 0, 0, 0);
+  }
+  const int dj = lane % SGD, dsub = lane / SGD;
+  const uint4 *d4 = reinterpret_cast<const uint4 *>(dw + (int64_t)(drow0 + dsub) * (F / 2));
+#pragma unroll
+  for (int i = 0; i < CPLD; ++i) {
+    const int c = i * SGD + dj;
+    cd[i] = (CPLD * SGD == UF || c < UF) ? load_stream16(d4 + c) : make_uint4(0, 0, 0, 0);
+  }
+}
+
 template <int D, int F, int K, bool PBIAS>
 __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
   using C = StackCfg<D, F, K, PBIAS>;
-  constexpr int NT = C::NT, U = C::U, NG = C::NG, SGU = C::SGU, CPLU = C::CPLU;
-  constexpr int RPSU = C::RPSU, ROWS_U = C::ROWS_U, SB_U4 = C::SB_U4;
+  constexpr int NT = C::NT, U = C::U, SB_U4 = C::SB_U4;
   constexpr int UF = C::UF, NGF = C::NGF, SGD = C::SGD, CPLD = C::CPLD;
-  constexpr int RPSD = C::RPSD, ROWS_D = C::ROWS_D, SBD_U4 = C::SBD_U4, NP = C::NP;
+  constexpr int ROWS_D = C::ROWS_D, SBD_U4 = C::SBD_U4, NP = C::NP;
+  constexpr int ROWS_U = C::ROWS_U, NPOS = F / ROWS_U;
   constexpr int XU4 = D / 8, HU4 = F / 8;
   constexpr int RIT = (XU4 + 63) / 64;       // router-row pieces per lane
+  constexpr int XIT = (XU4 + NT - 1) / NT;
+  constexpr int W_ROUTER = 6, W_RANK = 7;    // the router wave and the ranking wave
+  static_assert(C::WAVES_U <= W_ROUTER && NT / 64 == 8, "wave roles");
+  static_assert(C::ITEMS_U == K * NPOS, "one gate/up block per (position, row block)");
 
   __shared__ uint4 act_l[4 * U];
   __shared__ float asum_l[U];
@@ -199,34 +357,103 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
   __shared__ int sel_id[K];
   __shared__ float sel_sc[K];
   __shared__ int32_t sel_ref[K];
+  __shared__ int pred_buf[2][K];     // lookahead's K best, rank order (slot l & 1)
+  __shared__ int pred_cnt[2];
+  __shared__ int d_rank[K];          // D wave w: routing rank of its expert
+  __shared__ int d_fix[K];           // D wave w: fix-up slot, or -1 (predicted at w)
+  __shared__ int32_t miss_ref[K];    // fix-up slot -> slot ref
+  __shared__ int n_miss;
+  __shared__ int u_done[2];          // gate/up waves finished (slot l & 1)
+  __shared__ int staged[2];          // gate/up waves done staging x (slot l & 1)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wg = blockIdx.x;
   const uint32_t ep = a.epoch;
+  const int upos = wg / NPOS, urow0 = (wg % NPOS) * ROWS_U;   // gate/up block
+  const int drow0 = wg * ROWS_D;                               // down block
+  const int dj = lane % SGD, dsub = lane / SGD;
+  uint16_t *h_pred = a.h, *h_fix = a.h + (size_t)K * F;
+  if (tid < 2) {
+    pred_cnt[tid] = 0;               // layer 0 has no prediction
+    u_done[tid] = 0;
+    staged[tid] = 0;
+  }
+
+  // staged registers, carried from the end of one layer into the next
+  uint4 cg[C::CPLU], cu[C::CPLU], sr[C::SIT], cd[CPLD], sdr[C::SDIT];
+#pragma unroll
+  for (int i = 0; i < C::CPLU; ++i) cg[i] = cu[i] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < C::SIT; ++i) sr[i] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < CPLD; ++i) cd[i] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < C::SDIT; ++i) sdr[i] = make_uint4(0, 0, 0, 0);
 
   for (int l = 0; l < a.L; ++l) {
     const bool has_next = l + 1 < a.L;
     const int nrows = a.E * (has_next ? 2 : 1);
-    trace_mark(a, l, TR_START);
-    // ------------------------------------------------------------ R_l ----
-    if (wg < nrows) {
-      const bool nxt = wg >= a.E;
-      const int e = nxt ? wg - a.E : wg;
-      const int lw = nxt ? l + 1 : l;
-      // one wave per row, the lane partition and summation order of
-      // route_kernel, so both paths produce bit-identical logits
-      const uint4 *w4 = reinterpret_cast<const uint4 *>(a.W + ((size_t)lw * a.E + e) * D);
-      uint4 wr[RIT];
-      if (wave == 0) {
+    const int32_t *tab = a.table + (size_t)l * a.E;
+    if (wave == 0) trace_mark(a, l, TR_START);
+    // the router row's weights before the wait (wave 6)
+    uint4 wr[RIT];
+    const bool rrow = wave == W_ROUTER && wg < nrows;
+    const bool rnxt = wg >= a.E;
+    if (rrow) {
+      const int e = rnxt ? wg - a.E : wg;
+      const uint4 *w4 =
+          reinterpret_cast<const uint4 *>(a.W + ((size_t)(rnxt ? l + 1 : l) * a.E + e) * D);
 #pragma unroll
-        for (int it = 0; it < RIT; ++it) {
-          const int i = lane + it * 64;
-          wr[it] = (i < XU4) ? load_stream16(w4 + i) : make_uint4(0, 0, 0, 0);
-        }
+      for (int it = 0; it < RIT; ++it) {
+        const int i = lane + it * 64;
+        wr[it] = (i < XU4) ? load_stream16(w4 + i) : make_uint4(0, 0, 0, 0);
       }
-      if (l > 0) wg_wait(counter(a, l - 1, CNT_D), ep * C::ITEMS_D);
-      trace_mark(a, l, TR_R_WAITED);
-      if (wave == 0) {
+    }
+    // ------------------------------------------------------ layer start ----
+    if (l > 0) wg_wait(counter(a, l - 1, CNT_D), ep * C::ITEMS_D);
+    else __syncthreads();
+    if (wave == 0) trace_mark(a, l, TR_R_WAITED);
+    const int pcnt = pred_cnt[l & 1];
+    const int *P = pred_buf[l & 1];
+    // ------------------------------------------------------- role split ----
+    if (wave < W_ROUTER) {
+      // stage x_l (pair order + 32-input sums) and the predicted block's
+      // scales; the six gate/up waves then meet on an LDS counter, so the
+      // router and ranking waves never wait for the staging
+      static_assert(XIT == 1 && XU4 <= 64 * W_ROUTER && C::SIT == 1 &&
+                        4 * SB_U4 <= 64 * W_ROUTER, "staging by the gate/up waves");
+      {
+        const uint4 *x4 = reinterpret_cast<const uint4 *>(a.x + (size_t)l * D);
+        float s = 0.f;
+        if (tid < XU4) s = stage_piece<U>(act_l, tid, x4[tid]);
+        s += dpp_f<kDppQuadXor1>(s);
+        s += dpp_f<kDppQuadXor2>(s);
+        if (tid < XU4 && (tid & 3) == 0) asum_l[tid >> 2] = s;
+        if (upos < pcnt && tid < 4 * SB_U4) (&sbu_l[0][0])[tid] = sr[0];
+      }
+      if (lane == 0) {
+        __hip_atomic_fetch_add(&staged[l & 1], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        while (__hip_atomic_load(&staged[l & 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+               W_ROUTER)
+          __builtin_amdgcn_s_sleep(1);
+      }
+      __builtin_amdgcn_wave_barrier();
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      // gate/up of the predicted expert at this workgroup's position
+      if (wave < C::WAVES_U && upos < pcnt)
+        u_rows<C>(a, tab[P[upos]], urow0, cg, cu, act_l, asum_l, sbu_l,
+                  h_pred + (size_t)upos * F);
+      // the position's counter advances by NPOS every layer, work or not
+      __builtin_amdgcn_s_waitcnt(0);
+      if (lane == 0 && atomicAdd(&u_done[l & 1], 1) == W_ROUTER - 1)
+        __hip_atomic_fetch_add(counter(a, l, CNT_U0 + upos) + (wg % kSub) * 32, 1u,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (wave == 0) trace_mark(a, l, TR_U_ARRIVED);
+    } else if (wave == W_ROUTER) {
+      // one router row (the lane partition and summation order of
+      // route_kernel, so both paths produce bit-identical logits)
+      if (rrow) {
+        const int e = rnxt ? wg - a.E : wg;
         const uint4 *x4 = reinterpret_cast<const uint4 *>(a.x + (size_t)l * D);
         uint4 v[RIT];
 #pragma unroll
@@ -243,27 +470,45 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
           acc = dot2_bf16(wr[it].w, v[it].w, acc);
         }
         acc = group_sum<64>(acc);
-        if (lane == 0) st_dev(a.logits + (nxt ? a.E : 0) + e, acc);
+        if (lane == 0) st_dev(a.logits + (rnxt ? a.E : 0) + e, acc);
+        wave_arrive(counter(a, l, rnxt ? CNT_RL : CNT_R));
+        trace_mark(a, l, TR_R_ARRIVED);
       }
-      wg_arrive(counter(a, l, nxt ? CNT_RL : CNT_R));
-      trace_mark(a, l, TR_R_ARRIVED);
-    }
-    // ------------------------------------------------------ selection ----
-    // every workgroup needs this layer's router rows; only workgroup 0 waits
-    // for the lookahead rows (it publishes the predicted ids)
-    if (wave == 0 || (wave == 1 && has_next && wg == 0)) {
-      const bool la = wave == 1;
-      wave_wait(counter(a, l, la ? CNT_RL : CNT_R), ep * a.E);
-      if (!la) trace_mark(a, l, TR_R_ALL);
+      // lookahead ranking of layer l+1: raw bf16 logits of its router on x_l
+      if (has_next) {
+        wave_wait(counter(a, l, CNT_RL), ep * a.E);
+        const int e0 = lane, e1 = lane + 64;
+        const uint16_t *bias = a.bias ? a.bias + (size_t)(l + 1) * a.E : nullptr;
+        float z0 = -INFINITY, z1 = -INFINITY;
+        if (e0 < a.E) z0 = round_bf16(ld_dev(a.logits + a.E + e0) + (bias ? bf16_to_f32(bias[e0]) : 0.f));
+        if (e1 < a.E) z1 = round_bf16(ld_dev(a.logits + a.E + e1) + (bias ? bf16_to_f32(bias[e1]) : 0.f));
+        bool s0, s1;
+        int r0, r1;
+        select_topk(e0 < a.E ? order_key(z0) : -1, e1 < a.E ? order_key(z1) : -1, a.kp, lane,
+                    s0, s1, r0, r1);
+        if (wg == 0) {
+          if (s0) a.pred[(size_t)l * a.kp + r0] = e0;
+          if (s1) a.pred[(size_t)l * a.kp + r1] = e1;
+        }
+        int *pn = pred_buf[(l + 1) & 1];
+        if (s0 && r0 < K) pn[r0] = e0;
+        if (s1 && r1 < K) pn[r1] = e1;
+        if (lane == 0) pred_cnt[(l + 1) & 1] = min(a.kp, K);
+      }
+    } else {
+      // ---- routing: every workgroup ranks this layer's logits ----------
       const int e0 = lane, e1 = lane + 64;
-      const float *lg = a.logits + (la ? a.E : 0);
-      const uint16_t *bias = a.bias ? a.bias + (size_t)(la ? l + 1 : l) * a.E : nullptr;
+      const uint16_t *bias = a.bias ? a.bias + (size_t)l * a.E : nullptr;
+      const float b0 = (bias && e0 < a.E) ? bf16_to_f32(bias[e0]) : 0.f;   // before the wait
+      const float b1 = (bias && e1 < a.E) ? bf16_to_f32(bias[e1]) : 0.f;
+      wave_wait(counter(a, l, CNT_R), ep * a.E);
+      trace_mark(a, l, TR_R_ALL);
       float z0 = -INFINITY, z1 = -INFINITY;
-      if (e0 < a.E) z0 = round_bf16(ld_dev(lg + e0) + (bias ? bf16_to_f32(bias[e0]) : 0.f));
-      if (e1 < a.E) z1 = round_bf16(ld_dev(lg + e1) + (bias ? bf16_to_f32(bias[e1]) : 0.f));
-      if (!la) trace_mark_after(a, l, TR_LOGITS, z0 + z1);
+      if (e0 < a.E) z0 = round_bf16(ld_dev(a.logits + e0) + b0);
+      if (e1 < a.E) z1 = round_bf16(ld_dev(a.logits + e1) + b1);
+      trace_mark_after(a, l, TR_LOGITS, z0 + z1);
       float v0 = z0, v1 = z1;
-      if (!la && a.mode == MOE_ROUTE_SOFTMAX_TOPK) {
+      if (a.mode == MOE_ROUTE_SOFTMAX_TOPK) {
         const float m = wave_max(fmaxf(z0, z1));
         const float x0 = (e0 < a.E) ? expf(z0 - m) : 0.f;
         const float x1 = (e1 < a.E) ? expf(z1 - m) : 0.f;
@@ -271,252 +516,179 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
         v0 = round_bf16(x0 / s);
         v1 = round_bf16(x1 / s);
       }
-      if (!la) trace_mark_after(a, l, TR_SOFTMAX, v0 + v1);
-      const int kk = la ? a.kp : K;
+      trace_mark_after(a, l, TR_SOFTMAX, v0 + v1);
       bool s0, s1;
       int r0, r1;
-      select_topk(e0 < a.E ? order_key(v0) : -1, e1 < a.E ? order_key(v1) : -1, kk, lane,
+      select_topk(e0 < a.E ? order_key(v0) : -1, e1 < a.E ? order_key(v1) : -1, K, lane,
                   s0, s1, r0, r1);
-      if (!la) trace_mark_after(a, l, TR_TOPK, (float)(r0 + r1));
-      if (la) {
-        if (s0) a.pred[(size_t)l * a.kp + r0] = e0;
-        if (s1) a.pred[(size_t)l * a.kp + r1] = e1;
+      trace_mark_after(a, l, TR_TOPK, (float)(r0 + r1));
+      float sc0 = v0, sc1 = v1;
+      if (a.mode == MOE_ROUTE_SOFTMAX_TOPK) {
+        if (a.renorm) {
+          const float tot = round_bf16(group_sum<64>((s0 ? v0 : 0.f) + (s1 ? v1 : 0.f)));
+          sc0 = round_bf16(v0 / tot);
+          sc1 = round_bf16(v1 / tot);
+        }
       } else {
-        float sc0 = v0, sc1 = v1;
-        if (a.mode == MOE_ROUTE_SOFTMAX_TOPK) {
-          if (a.renorm) {
-            const float tot = round_bf16(group_sum<64>((s0 ? v0 : 0.f) + (s1 ? v1 : 0.f)));
-            sc0 = round_bf16(v0 / tot);
-            sc1 = round_bf16(v1 / tot);
-          }
+        const float m = wave_max(fmaxf(s0 ? z0 : -INFINITY, s1 ? z1 : -INFINITY));
+        const float x0 = s0 ? expf(z0 - m) : 0.f;
+        const float x1 = s1 ? expf(z1 - m) : 0.f;
+        const float s = group_sum<64>(x0 + x1);
+        sc0 = round_bf16(x0 / s);
+        sc1 = round_bf16(x1 / s);
+      }
+      if (s0) {
+        sel_id[r0] = e0;
+        sel_sc[r0] = sc0;
+        sel_ref[r0] = tab[e0];
+      }
+      if (s1) {
+        sel_id[r1] = e1;
+        sel_sc[r1] = sc1;
+        sel_ref[r1] = tab[e1];
+      }
+      // ---- which D wave takes which routed expert -----------------------
+      // Predicted position w keeps its expert if it was routed (its codes
+      // are staged there); the routed experts that were not predicted go,
+      // in rank order, to the other positions in order (fix-up slots).
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_wave_barrier();
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+      bool miss = false, routed = false;
+      int rank_w = -1;
+      int32_t ref_r = 0;
+      if (lane < K) {
+        const int er = sel_id[lane];   // routed expert of rank `lane`
+        ref_r = sel_ref[lane];
+        miss = true;
+        for (int p = 0; p < pcnt; ++p) miss = miss && (P[p] != er);
+        const int pw = lane < pcnt ? P[lane] : -1;   // predicted expert at position `lane`
+        for (int r = 0; r < K; ++r)
+          if (pw >= 0 && sel_id[r] == pw) { routed = true; rank_w = r; }
+      }
+      const uint64_t mm = __ballot(miss), fm = __ballot(lane < K && !routed);
+      if (miss) miss_ref[__popcll(mm & below)] = ref_r;
+      if (lane < K) {
+        if (routed) {
+          d_rank[lane] = rank_w;
+          d_fix[lane] = -1;
         } else {
-          const float m = wave_max(fmaxf(s0 ? z0 : -INFINITY, s1 ? z1 : -INFINITY));
-          const float x0 = s0 ? expf(z0 - m) : 0.f;
-          const float x1 = s1 ? expf(z1 - m) : 0.f;
-          const float s = group_sum<64>(x0 + x1);
-          sc0 = round_bf16(x0 / s);
-          sc1 = round_bf16(x1 / s);
-        }
-        const int32_t *tab = a.table + (size_t)l * a.E;
-        if (s0) {
-          sel_id[r0] = e0;
-          sel_sc[r0] = sc0;
-          sel_ref[r0] = tab[e0];
-        }
-        if (s1) {
-          sel_id[r1] = e1;
-          sel_sc[r1] = sc1;
-          sel_ref[r1] = tab[e1];
+          const int fi = __popcll(fm & below);
+          uint64_t m = mm;
+          for (int i = 0; i < fi; ++i) m &= m - 1;
+          d_rank[lane] = (int)__builtin_ctzll(m);
+          d_fix[lane] = fi;
         }
       }
+      if (lane == 0) n_miss = __popcll(mm);
     }
     __syncthreads();
+    if (wave == 0) trace_mark(a, l, TR_SELECTED);
+    if (tid == 0) {   // next layer's slots; nobody touches them before its start
+      u_done[(l + 1) & 1] = 0;
+      staged[(l + 1) & 1] = 0;
+    }
     if (wg == 0 && tid < K) {
       a.ids[(size_t)l * K + tid] = sel_id[tid];
       a.scores[(size_t)l * K + tid] = sel_sc[tid];
       a.refs_out[(size_t)l * K + tid] = sel_ref[tid];
       if (sel_ref[tid] < 0) atomicAdd(a.miss + l, 1);
     }
-
-    trace_mark(a, l, TR_SELECTED);
-
-    // ------------------------------------------------------------ U_l ----
-    if (wg < C::ITEMS_U) {
-      const int pj = wg / (F / ROWS_U), rb = wg % (F / ROWS_U);
-      const int32_t ref = sel_ref[pj];
-      const int row0 = rb * ROWS_U;
-      const char *gw = resolve(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref);
-      const char *uw = resolve(a.pa, comp_index(PROJ_UP, PART_W, NP), ref);
-      const bool ok = gw != nullptr;
-      const bool uwave = wave < C::WAVES_U;
-      const int uj = lane % SGU, usub = lane / SGU;
-      // small loads first: x pieces and the block's scales/biases
-      constexpr int XIT = (XU4 + NT - 1) / NT, SIT = (4 * SB_U4 + NT - 1) / NT;
-      uint4 xr[XIT], sr[SIT];
-      const uint4 *x4 = reinterpret_cast<const uint4 *>(a.x + (size_t)l * D);
+    // ------------------------------------------ fix-up: unpredicted ----
+    {
+      const int mi = upos;       // this workgroup's fix-up slot and rows
+      if (mi < n_miss) {
+        const int32_t ref = miss_ref[mi];
+        u_load<C>(a, ref, urow0, cg, cu, sr);
 #pragma unroll
-      for (int it = 0; it < XIT; ++it) {
-        const int i = it * NT + tid;
-        xr[it] = (i < XU4) ? x4[i] : make_uint4(0, 0, 0, 0);
-      }
-      if (ok) {
-#pragma unroll
-        for (int it = 0; it < SIT; ++it) {
-          const int i = it * NT + tid;
-          const int p = i / SB_U4, o = i % SB_U4;
-          const int part = (p & 1) ? PART_B : PART_S, proj = (p >> 1) ? PROJ_UP : PROJ_GATE;
-          const char *sp = resolve(a.pa, comp_index(proj, part, NP), ref);
-          sr[it] = (i < 4 * SB_U4)
-                       ? reinterpret_cast<const uint4 *>(sp + (int64_t)row0 * NG * 2)[o]
-                       : make_uint4(0, 0, 0, 0);
-        }
-      }
-      uint4 cg[CPLU], cu[CPLU];
-      const int urow = row0 + wave * RPSU + usub;
-      if (ok && uwave) {
-        const uint4 *g4 = reinterpret_cast<const uint4 *>(gw + (int64_t)urow * (D / 2));
-        const uint4 *u4 = reinterpret_cast<const uint4 *>(uw + (int64_t)urow * (D / 2));
-#pragma unroll
-        for (int i = 0; i < CPLU; ++i) {
-          cg[i] = load_stream16(g4 + i * SGU + uj);
-          cu[i] = load_stream16(u4 + i * SGU + uj);
-        }
-      }
-      if (ok) {
-#pragma unroll
-        for (int it = 0; it < SIT; ++it) {
+        for (int it = 0; it < C::SIT; ++it) {
           const int i = it * NT + tid;
           if (i < 4 * SB_U4) (&sbu_l[0][0])[i] = sr[it];
         }
+        __syncthreads();
+        if (wave < C::WAVES_U)
+          u_rows<C>(a, ref, urow0, cg, cu, act_l, asum_l, sbu_l, h_fix + (size_t)mi * F);
       }
-#pragma unroll
-      for (int it = 0; it < XIT; ++it) {
-        const int i = it * NT + tid;
-        float s = 0.f;
-        if (i < XU4) s = stage_piece<U>(act_l, i, xr[it]);
-        s += dpp_f<kDppQuadXor1>(s);
-        s += dpp_f<kDppQuadXor2>(s);
-        if (i < XU4 && (i & 3) == 0) asum_l[i >> 2] = s;
-      }
-      __syncthreads();
-      if (uwave) {
-        float pg = 0.f, pu = 0.f;
-        if (ok) {
-          const uint16_t *sbh = reinterpret_cast<const uint16_t *>(&sbu_l[0][0]);
-          constexpr int SBN = SB_U4 * 8;
-          const int rl = wave * RPSU + usub;
-#pragma unroll
-          for (int i = 0; i < CPLU; ++i) {
-            const int c = i * SGU + uj;
-            const int g = rl * NG + (c >> 1);
-            const float Sg = bf16_to_f32(sbh[g]), Bg = bf16_to_f32(sbh[SBN + g]);
-            const float Su = bf16_to_f32(sbh[2 * SBN + g]), Bu = bf16_to_f32(sbh[3 * SBN + g]);
-            const float xs = asum_l[c];
-            pg += Sg * chunk_dot_lds<U>(cg[i], act_l, c) + (Bg - 128.f * Sg) * xs;
-            pu += Su * chunk_dot_lds<U>(cu[i], act_l, c) + (Bu - 128.f * Su) * xs;
-          }
-        }
-        pg = group_sum<SGU>(pg);
-        pu = group_sum<SGU>(pu);
-        if (uj == 0) {
-          float hv = 0.f;
-          if (ok) {
-            if (PBIAS) {
-              pg += bf16_to_f32(reinterpret_cast<const uint16_t *>(
-                  resolve(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref))[urow]);
-              pu += bf16_to_f32(reinterpret_cast<const uint16_t *>(
-                  resolve(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref))[urow]);
-            }
-            hv = apply_act(a.act, pg, pu, a.alpha, a.limit);
-          } else if (lane == 0) {
-            flag_error();
-          }
-          st_dev(a.h + (size_t)pj * F + urow, round_bf16(hv));   // h is bf16-valued
-        }
-      }
-      wg_arrive(counter(a, l, CNT_U0 + pj));
-      trace_mark(a, l, TR_U_ARRIVED);
+      wg_arrive(counter(a, l, CNT_F0 + mi));
+      if (wave == 0) trace_mark(a, l, TR_FIXED);
     }
-
-    // ------------------------------------------- D_l codes (prefetch) ----
-    // this workgroup's down item: output rows wg*8 .. +8, wave = expert;
-    // issued after the gate/up arrival (which waits for all of its own
-    // memory operations) and before the wait for the activations
-    const bool has_d = wg < C::ITEMS_D && wave < K;
-    const int32_t dref = has_d ? sel_ref[wave] : 0;
-    const char *dw = has_d ? resolve(a.pa, comp_index(PROJ_DOWN, PART_W, NP), dref) : nullptr;
-    const int drow0 = wg * ROWS_D;
-    const int dj = lane % SGD, dsub = lane / SGD;
-    uint4 cd[CPLD];
-    uint4 sdr[(2 * SBD_U4 + 63) / 64];
-    if (dw != nullptr) {
-#pragma unroll
-      for (int it = 0; it < (2 * SBD_U4 + 63) / 64; ++it) {
-        const int i = it * 64 + lane;
-        const int p = i / SBD_U4, o = i % SBD_U4;
-        const char *sp = resolve(a.pa, comp_index(PROJ_DOWN, p ? PART_B : PART_S, NP), dref);
-        sdr[it] = (i < 2 * SBD_U4)
-                      ? reinterpret_cast<const uint4 *>(sp + (int64_t)drow0 * NGF * 2)[o]
-                      : make_uint4(0, 0, 0, 0);
-      }
-      const uint4 *d4 = reinterpret_cast<const uint4 *>(dw + (int64_t)(drow0 + dsub) * (F / 2));
-#pragma unroll
-      for (int i = 0; i < CPLD; ++i) {
-        const int c = i * SGD + dj;
-        cd[i] = (CPLD * SGD == UF || c < UF) ? load_stream16(d4 + c) : make_uint4(0, 0, 0, 0);
-      }
-    }
-
     // ------------------------------------------------------------ D_l ----
-    if (wg < C::ITEMS_D) {
-      if (wave < K) {
-        // this wave's expert: its activations are complete when the expert's
-        // gate/up workgroups have all arrived
-        wave_wait(counter(a, l, CNT_U0 + wave), ep * (F / ROWS_U));
-        if (wave == 0) trace_mark(a, l, TR_D_WAITED);
-        uint4 *hact = hact_l[wave];
-        float *hsum = hsum_l[wave];
-        if (dw != nullptr) {
-          uint4 *sbd = sbd_l[wave];
+    if (wave < K) {
+      const int r = d_rank[wave], fx = d_fix[wave];
+      const int32_t dref = sel_ref[r];
+      const char *dw = resolve(a.pa, comp_index(PROJ_DOWN, PART_W, NP), dref);
+      if (fx >= 0) d_load<C>(a, dref, drow0, cd, sdr);   // not staged
+      wave_wait(counter(a, l, fx < 0 ? CNT_U0 + wave : CNT_F0 + fx), ep * NPOS);
+      if (wave == 0) trace_mark(a, l, TR_D_WAITED);
+      uint4 *hact = hact_l[wave];
+      float *hsum = hsum_l[wave];
+      if (dw != nullptr) {
+        uint4 *sbd = sbd_l[wave];
 #pragma unroll
-          for (int it = 0; it < (2 * SBD_U4 + 63) / 64; ++it) {
-            const int i = it * 64 + lane;
-            if (i < 2 * SBD_U4) sbd[i] = sdr[it];
-          }
-          const float *hrow = a.h + (size_t)wave * F;
-#pragma unroll
-          for (int it = 0; it < (HU4 + 63) / 64; ++it) {
-            const int i = it * 64 + lane;
-            float s = 0.f;
-            if (i < HU4) {
-              const uint4 lo = ld_dev16(hrow + 8 * i), hi = ld_dev16(hrow + 8 * i + 4);
-              // bf16-valued floats: the high halves are the bf16 bit patterns
-              const uint4 wds = make_uint4((lo.x >> 16) | (lo.y & 0xffff0000u),
-                                           (lo.z >> 16) | (lo.w & 0xffff0000u),
-                                           (hi.x >> 16) | (hi.y & 0xffff0000u),
-                                           (hi.z >> 16) | (hi.w & 0xffff0000u));
-              s = stage_piece<UF>(hact, i, wds);
-            }
-            s += dpp_f<kDppQuadXor1>(s);
-            s += dpp_f<kDppQuadXor2>(s);
-            if (i < HU4 && (i & 3) == 0) hsum[i >> 2] = s;
-          }
-        } else if (has_d && lane == 0) {
-          flag_error();
+        for (int it = 0; it < C::SDIT; ++it) {
+          const int i = it * 64 + lane;
+          if (i < 2 * SBD_U4) sbd[i] = sdr[it];
         }
-      }
-      __syncthreads();
-      if (wave < K) {
-        float p = 0.f;
-        if (dw != nullptr) {
-          const uint16_t *sbh = reinterpret_cast<const uint16_t *>(sbd_l[wave]);
-          constexpr int SBN = SBD_U4 * 8;
+        const uint16_t *hrow = (fx < 0 ? h_pred + (size_t)wave * F : h_fix + (size_t)fx * F);
+        // the expert's F activations: 8 bf16 per 16-byte piece, <= 2 per lane
+        static_assert(HU4 <= 128, "two pieces per lane");
+        const int i0 = lane, i1 = lane + 64;
+        uint4 p0, p1;
+        ld_dev_b128x2(hrow + 8 * min(i0, HU4 - 1), hrow + 8 * min(i1, HU4 - 1), p0, p1);
 #pragma unroll
-          for (int i = 0; i < CPLD; ++i) {
-            const int c = i * SGD + dj;
-            if (CPLD * SGD == UF || c < UF) {
-              const int g = dsub * NGF + (c >> 1);
-              const float Sd = bf16_to_f32(sbh[g]), Bd = bf16_to_f32(sbh[SBN + g]);
-              p += Sd * chunk_dot_lds<UF>(cd[i], hact_l[wave], c) + (Bd - 128.f * Sd) * hsum_l[wave][c];
-            }
+        for (int it = 0; it < 2; ++it) {
+          const int i = it ? i1 : i0;
+          float s = 0.f;
+          if (i < HU4) s = stage_piece<UF>(hact, i, it ? p1 : p0);
+          s += dpp_f<kDppQuadXor1>(s);
+          s += dpp_f<kDppQuadXor2>(s);
+          if (i < HU4 && (i & 3) == 0) hsum[i >> 2] = s;
+        }
+      } else if (lane == 0) {
+        flag_error();
+      }
+      // same-wave LDS handoff: staging above, reads below
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_wave_barrier();
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      float p = 0.f;
+      if (dw != nullptr) {
+        const uint16_t *sbh = reinterpret_cast<const uint16_t *>(sbd_l[wave]);
+        constexpr int SBN = SBD_U4 * 8;
+#pragma unroll
+        for (int i = 0; i < CPLD; ++i) {
+          const int c = i * SGD + dj;
+          if (CPLD * SGD == UF || c < UF) {
+            const int g = dsub * NGF + (c >> 1);
+            const float Sd = bf16_to_f32(sbh[g]), Bd = bf16_to_f32(sbh[SBN + g]);
+            p += Sd * chunk_dot_lds<UF>(cd[i], hact_l[wave], c) + (Bd - 128.f * Sd) * hsum_l[wave][c];
           }
         }
-        p = group_sum<SGD>(p);
-        if (dj == 0) {
-          if (PBIAS && dw != nullptr)
-            p += bf16_to_f32(reinterpret_cast<const uint16_t *>(
-                resolve(a.pa, comp_index(PROJ_DOWN, PART_BIAS, NP), dref))[drow0 + dsub]);
-          red_l[wave][dsub] = (dw != nullptr) ? sel_sc[wave] * p : 0.f;
-        }
       }
-      __syncthreads();
-      if (tid < ROWS_D) {
-        float yv = 0.f;
-        for (int w = 0; w < K; ++w) yv += red_l[w][tid];   // expert order
-        a.y[(size_t)l * D + drow0 + tid] = (uint16_t)f32_to_bf16(yv);
+      p = group_sum<SGD>(p);
+      if (dj == 0) {
+        if (PBIAS && dw != nullptr)
+          p += bf16_to_f32(reinterpret_cast<const uint16_t *>(
+              resolve(a.pa, comp_index(PROJ_DOWN, PART_BIAS, NP), dref))[drow0 + dsub]);
+        red_l[r][dsub] = (dw != nullptr) ? sel_sc[r] * p : 0.f;
       }
-      wg_arrive(counter(a, l, CNT_D));
-      trace_mark(a, l, TR_D_ARRIVED);
+    }
+    __syncthreads();
+    if (tid < ROWS_D) {
+      float yv = 0.f;
+      for (int w = 0; w < K; ++w) yv += red_l[w][tid];   // rank order
+      a.y[(size_t)l * D + drow0 + tid] = (uint16_t)f32_to_bf16(yv);
+    }
+    wg_arrive(counter(a, l, CNT_D));
+    if (wave == 0) trace_mark(a, l, TR_D_ARRIVED);
+    // ----------------------------- staging loads of layer l+1's prediction
+    if (has_next) {
+      const int pc = pred_cnt[(l + 1) & 1];
+      const int *Pn = pred_buf[(l + 1) & 1];
+      const int32_t *tabn = a.table + (size_t)(l + 1) * a.E;
+      if (upos < pc) u_load<C>(a, tabn[Pn[upos]], urow0, cg, cu, sr);
+      if (wave < K && wave < pc) d_load<C>(a, tabn[Pn[wave]], drow0, cd, sdr);
     }
   }
 }
