@@ -410,7 +410,10 @@ def main():
             "avg_us": round(avg_ms * 1e3, 3), "median_us": round(med_ms * 1e3, 3),
             "launches": n}
     block_bytes = stack.expert_bytes_per_token()
-    out = {"metric": "MoE decode tok/s (bs=1, 48 layers) + gather_qmm achieved HBM GB/s vs peak",
+    metric = ("MoE decode tok/s (bs=1, 48 layers) + gather_qmm achieved HBM GB/s vs peak"
+              if args.workload == "qwen3-48l" else
+              "MoE decode tok/s (bs=1, 36 layers, gpt-oss-120b shape) + achieved HBM GB/s vs peak")
+    out = {"metric": metric,
            "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
