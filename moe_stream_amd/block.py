@@ -78,8 +78,6 @@ def streaming_call(self: MoEBlock, x: torch.Tensor) -> torch.Tensor:
     shape = x.shape
     xt = x.reshape(-1, shape[-1]).contiguous()
     T, k = xt.shape[0], self.top_k
-    if T > 16:
-        raise ValueError("the decode path takes up to 16 tokens per call")
     # route + one lookahead in a single launch; further depths launch again
     preds = []
     tgt0 = layer + self.depths[0]
@@ -114,5 +112,6 @@ def streaming_call(self: MoEBlock, x: torch.Tensor) -> torch.Tensor:
     slots = np.asarray(pool.acquire(layer, uniq), dtype=np.int32)
     refs = (slots if inverse is None else slots[inverse]).reshape(T, k)
     refs_d = torch.from_numpy(np.ascontiguousarray(refs)).to(xt.device, non_blocking=True)
-    y = ops.ffn_decode(pool, refs_d, b.scores, xt)
+    # decode kernels for a few tokens, the grouped MFMA block for prefill
+    y = ops.ffn(pool, refs_d, b.scores, xt)
     return y.reshape(shape)

@@ -93,3 +93,27 @@ def test_lookahead_recall_is_measured(world):
     _, blocks, _ = _run(geom, store, W, xs, n_slots=300)
     rec = [r for b in blocks for r in b.recall]
     assert rec and all(0.0 <= r <= 1.0 for r in rec)
+
+
+def test_prefill_through_the_block(world):
+    """T = 40 tokens in one call (the prefill path: many-token router, np.unique
+    + inverse index build, grouped MFMA block) against the batched oracle."""
+    geom, store, W, _, host = world
+    pool = ExpertPool(geom, 200, store, n_layers=L)
+    blocks = _blocks(geom, pool, W)
+    xs = synth.hidden_states(40, L, geom.d_model, "cuda", 20260504)
+    x = xs[:, 1].contiguous()                     # 40 tokens at layer 1
+    y = blocks[1](x)
+    torch.cuda.synchronize()
+    X = bf16_values(x)
+    Z = N.router_logits(X, bf16_bits(W)[1], None, "mlx")
+    ids, sc = [], []
+    for t in range(40):
+        i, s, _ = N.top_k_experts(Z[t], 8, True, "mlx")
+        ids.append(i)
+        sc.append(s)
+    ref = N.moe_block_batch(X, np.array(ids), np.array(sc),
+                            lambda e: OL.split_record(host[1 * 128 + e], 2048, 768, False),
+                            "qwen3", "mlx")
+    err = max(N.rel_err(bf16_values(y[t]), ref[t]) for t in range(40))
+    assert err < TOL, err
