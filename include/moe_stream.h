@@ -197,9 +197,9 @@ int moe_route(const uint16_t *x, int32_t T, int32_t d_model,
  */
 size_t moe_stack_workspace(const moe_geom *g, int32_t n_layers, int32_t E, int32_t k);
 /* Phase trace of moe_stack_decode: while set, each launch writes wall-clock
- * stamps (wall_clock64 ticks) of the first 8 workgroups at the 8 phase
- * points of every layer into device_buf ([8][n_layers][8] uint64).  NULL
- * turns it off.  Process-wide setting. */
+ * stamps (wall_clock64 ticks, 100 MHz) of every workgroup (up to 256) at the
+ * 12 phase points of every layer into device_buf ([256][n_layers][12]
+ * uint64).  NULL turns it off.  Process-wide setting. */
 int moe_stack_trace(void *device_buf, size_t bytes);
 int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_layers,
                      int32_t E, int32_t k, const uint16_t *x, const uint16_t *W,

@@ -67,7 +67,7 @@ struct StackArgs {
 
 // Phase trace: wall-clock stamps of thread 0 of the first kTraceWGs
 // workgroups at each phase boundary of each layer.
-constexpr int kTraceWGs = 8;
+constexpr int kTraceWGs = 256;
 constexpr int kTracePoints = 12;
 enum { TR_START, TR_R_WAITED, TR_R_ARRIVED, TR_SELECTED, TR_U_ARRIVED,
        TR_D_WAITED, TR_D_ARRIVED, TR_R_ALL, TR_LOGITS, TR_SOFTMAX, TR_TOPK, TR_FIXED };
