@@ -33,11 +33,14 @@ def parse():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--tokens", type=int, default=64)
     ap.add_argument("--workload", default="qwen3-48l",
-                    choices=["qwen3-48l", "gptoss-36l", "qwen3-prefill", "qwen3-stream"],
+                    choices=["qwen3-48l", "gptoss-36l", "qwen3-prefill", "qwen3-stream",
+                             "hbm-copy"],
                     help="qwen3-prefill: 512 tokens per layer through the grouped "
                          "MFMA path; qwen3-stream: 256 decode tokens over a 2048-slot "
-                         "pool fed from a pinned host store (secondary measurements, "
-                         "not the headline)")
+                         "pool fed from a pinned host store; hbm-copy: a 1 GiB device "
+                         "copy, the achievable HBM rate and the known-size reference "
+                         "for the FETCH_SIZE / WRITE_SIZE counters (secondary "
+                         "measurements, not the headline)")
     ap.add_argument("--mode", default="persistent", choices=["persistent", "graph", "eager"],
                     help="persistent: one launch per token; graph/eager: 3 launches per layer")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -70,6 +73,24 @@ def workload(args, device):
 
 
 MFMA_BF16_PEAK_TFS = 2500.0   # MI355X dense bf16 MFMA
+
+# HBM bytes per launch measured with the L2 FETCH_SIZE / WRITE_SIZE counters
+# (each scaled by its reading for a copy of known size); the summary and the
+# commands that produced it are in the named file.
+TRAFFIC_FILES = {("qwen3-48l", "persistent"): "profiles/stack_decode_qwen3_48l_traffic.md"}
+
+
+def measured_traffic(workload, mode):
+    import re
+    name = TRAFFIC_FILES.get((workload, mode))
+    if name is None:
+        return None, None
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), name)
+    try:
+        m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", open(path).read(), re.M)
+    except OSError:
+        return None, None
+    return (int(m.group(1)), name) if m else (None, None)
 
 
 def prefill(args):
@@ -154,6 +175,41 @@ def prefill(args):
                         "avg_block_us": round(float(block_ms.mean()) * 1e3, 2)},
            "expert_weight_GBs": round(wbytes / block_s / 1e9, 1),
            "wall_s": round(wall, 3)}
+    print(json.dumps(out), flush=True)
+
+
+def hbm_copy(args):
+    """A 1 GiB device-to-device copy (1 GiB read + 1 GiB written per launch,
+    4x the 256 MB last-level cache) and a 1 GiB sum (read only): the
+    achievable HBM rates on this GPU, and the launch of known size that
+    scales the L2 FETCH_SIZE / WRITE_SIZE counters into bytes."""
+    import torch
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device=dev).random_(0, 255)
+    dst = torch.empty_like(src)
+    acc = src.view(torch.float32)
+    res = {}
+    for name, fn, nbytes in (("copy", lambda: dst.copy_(src), 2 * n),
+                             ("read", lambda: acc.sum(), n)):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(args.steps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / args.steps
+        res[name] = {"bytes_per_launch": nbytes, "avg_us": round(ms * 1e3, 1),
+                     "GBs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    out = {"metric": "achievable HBM GB/s (device copy, device sum)",
+           "value": res["copy"]["GBs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "higher_is_better": True, "dtype": "u8",
+           "data": "synthetic", "config": {"workload": "hbm-copy-1GiB"},
+           "peak": HBM_PEAK_GBS, **res}
     print(json.dumps(out), flush=True)
 
 
@@ -329,6 +385,8 @@ def main():
         return prefill(args)
     if args.workload == "qwen3-stream":
         return stream(args)
+    if args.workload == "hbm-copy":
+        return hbm_copy(args)
     import torch
     from moe_stream_amd import synth
     dev = torch.device("cuda:0")
@@ -404,9 +462,10 @@ def main():
         avg_ms, med_ms, n = time_dominant_kernel(stack, xs, min(args.profile_tokens, args.tokens))
         kname = "ffn_gate_up_kernel"
     achieved = per_launch / (avg_ms * 1e-3) / 1e9
+    traffic, traffic_src = measured_traffic(args.workload, mode)
     roof = {"bound": "hbm", "kernel": kname, "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None, "bytes_per_launch": per_launch,
+            "traffic": traffic, "traffic_source": traffic_src, "bytes_per_launch": per_launch,
             "avg_us": round(avg_ms * 1e3, 3), "median_us": round(med_ms * 1e3, 3),
             "launches": n}
     block_bytes = stack.expert_bytes_per_token()

@@ -1,6 +1,7 @@
 // C ABI of the expert hot path: argument checks, geometry dispatch, slot
 // fills, pinned host memory and events.  No exceptions cross this boundary;
 // failures return a negative status and set a thread-local message.
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -102,6 +103,8 @@ int make_pool_args(const moe_pool_view *v, const moe_geom *g, moe::PoolArgs *pa)
   if (v->n_records > INT32_MAX) return fail(MOE_ERR_INVALID, "too many store records");
   pa->n_records = v->store ? (int32_t)v->n_records : 0;
   pa->n_slots = v->n_slots;
+  if (pa->n_slots == 0 && pa->n_records == 0)
+    return fail(MOE_ERR_INVALID, "pool view has neither slots nor store records");
   return MOE_OK;
 }
 
@@ -426,6 +429,61 @@ int moe_slot_lookup(const int32_t *table, int32_t E, const int32_t *ids,
   return MOE_OK;
 }
 
+namespace {
+
+// Device-to-device slot fills, one launch per batch of up to kFillBatch
+// (record, slot) pairs carried in the kernel arguments (no index upload).
+// Workgroup (pair, chunk): chunk y of the pair's record, counted over its
+// components in order, kFillChunk bytes each, copied by 16-byte loads and
+// stores.
+constexpr int kFillBatch = 160;
+constexpr int64_t kFillChunk = 64 * 1024;
+
+struct FillArgs {
+  char *base[MOE_MAX_COMPONENTS];
+  int64_t slot_bytes[MOE_MAX_COMPONENTS];
+  int64_t src_offset[MOE_MAX_COMPONENTS];
+  int32_t chunk0[MOE_MAX_COMPONENTS + 1];   // first chunk of each component
+  const char *src;
+  int64_t record_bytes;
+  int32_t nc, n;
+  int32_t slot[kFillBatch];
+  int64_t rec[kFillBatch];
+};
+
+__global__ __launch_bounds__(256) void fill_slots_kernel(const FillArgs a) {
+  const int i = blockIdx.x, y = blockIdx.y;
+  int c = 0;
+  while (c + 1 < a.nc && y >= a.chunk0[c + 1]) ++c;
+  const int64_t off = (int64_t)(y - a.chunk0[c]) * kFillChunk;
+  const int64_t len = min(kFillChunk, a.slot_bytes[c] - off);
+  const uint4 *s = reinterpret_cast<const uint4 *>(a.src + a.rec[i] * a.record_bytes +
+                                                   a.src_offset[c] + off);
+  uint4 *d = reinterpret_cast<uint4 *>(a.base[c] + (int64_t)a.slot[i] * a.slot_bytes[c] + off);
+  const int n16 = (int)(len / 16);
+  constexpr int U = 4;
+  int j = threadIdx.x;
+  for (; j + (U - 1) * 256 < n16; j += U * 256) {
+    uint4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = s[j + u * 256];
+#pragma unroll
+    for (int u = 0; u < U; ++u) d[j + u * 256] = v[u];
+  }
+  for (; j < n16; j += 256) d[j] = s[j];
+}
+
+bool device_memory(const void *p) {
+  hipPointerAttribute_t at;
+  if (hipPointerGetAttributes(&at, p) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return at.type == hipMemoryTypeDevice;
+}
+
+}  // namespace
+
 int moe_fill_slots(const moe_pool_view *pool, const void *src_store,
                    int64_t src_record_bytes, const int64_t *src_records,
                    const int32_t *dst_slots, int32_t n, void *stream) {
@@ -446,6 +504,39 @@ int moe_fill_slots(const moe_pool_view *pool, const void *src_store,
       return fail(MOE_ERR_INVALID, "slot %d outside [0, %d)", slot, pool->n_slots);
     if (rec < 0 || (!src_store && rec >= pool->n_records))
       return fail(MOE_ERR_INVALID, "record %lld out of range", (long long)rec);
+  }
+  // a device-resident source with 16-byte aligned pieces: copy kernels
+  bool kernel = device_memory(src) && aligned(src, 16) && rb % 16 == 0;
+  FillArgs fa{};
+  int32_t chunks = 0;
+  for (int c = 0; c < nc && kernel; ++c) {
+    kernel = aligned(pool->base[c], 16) && pool->slot_bytes[c] % 16 == 0 &&
+             pool->comp_offset[c] % 16 == 0 && pool->comp_offset[c] + pool->slot_bytes[c] <= rb;
+    fa.base[c] = static_cast<char *>(pool->base[c]);
+    fa.slot_bytes[c] = pool->slot_bytes[c];
+    fa.src_offset[c] = pool->comp_offset[c];
+    fa.chunk0[c] = chunks;
+    chunks += (int32_t)((pool->slot_bytes[c] + kFillChunk - 1) / kFillChunk);
+  }
+  if (kernel) {
+    fa.chunk0[nc] = chunks;
+    fa.src = src;
+    fa.record_bytes = rb;
+    fa.nc = nc;
+    for (int32_t i0 = 0; i0 < n; i0 += kFillBatch) {
+      fa.n = std::min<int32_t>(kFillBatch, n - i0);
+      for (int32_t i = 0; i < fa.n; ++i) {
+        fa.slot[i] = dst_slots[i0 + i];
+        fa.rec[i] = src_records[i0 + i];
+      }
+      hipLaunchKernelGGL(fill_slots_kernel, dim3(fa.n, chunks), dim3(256), 0, s, fa);
+      MOE_HIP(hipGetLastError());
+    }
+    return MOE_OK;
+  }
+  for (int32_t i = 0; i < n; ++i) {
+    const int32_t slot = dst_slots[i];
+    const int64_t rec = src_records[i];
     for (int c = 0; c < nc; ++c) {
       // each component's size is its slot stride in the pool
       MOE_HIP(hipMemcpyAsync(static_cast<char *>(pool->base[c]) + slot * pool->slot_bytes[c],

@@ -16,9 +16,26 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // 16-byte streaming load (weights are read once per launch).
+// 16 bytes as one vector load into registers.  (Assigning the uint4 struct
+// from memory is lowered to a memcpy that can keep a small array of them in
+// scratch, whose later reload waits for every load issued before it.)
+__device__ __forceinline__ uint4 load16(const uint4 *p) {
+  u32x4_t v = *reinterpret_cast<const u32x4_t *>(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ uint4 load_stream16(const uint4 *p) {
   u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Keep memory instructions in program order across this point, both in the
+// compiler's IR passes (the empty asm with a memory clobber) and in the
+// machine scheduler (the scheduling barrier).  Emits no instruction and no
+// wait: the loads issued before it stay in flight.
+__device__ __forceinline__ void issue_order_fence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 // --- bf16 <-> f32 -----------------------------------------------------------
@@ -155,6 +172,17 @@ __device__ __forceinline__ const char *resolve(const PoolArgs &pa, int c,
   int64_t r = -(int64_t)ref - 1;
   if (pa.store == nullptr || r >= pa.n_records) return nullptr;
   return pa.store + r * pa.record_bytes + pa.comp_offset[c];
+}
+
+// As resolve(), but an out-of-range reference yields slot 0 (or store record
+// 0 when the pool has no slots; the host rejects a pool with neither) and
+// clears `ok`: the kernel reads valid memory with no branch around its
+// loads, then flags the error and contributes nothing.
+__device__ __forceinline__ const char *resolve_safe(const PoolArgs &pa, int c, int32_t ref,
+                                                    bool &ok) {
+  const char *p = resolve(pa, c, ref);
+  ok = p != nullptr;
+  return ok ? p : (pa.n_slots > 0 ? pa.base[c] : pa.store + pa.comp_offset[c]);
 }
 
 __device__ __forceinline__ void flag_error() {

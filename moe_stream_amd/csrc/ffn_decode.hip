@@ -126,26 +126,46 @@ __global__ __launch_bounds__(WAVES * 64) void ffn_gate_up_kernel(
   uint4 xr[XIT], sr[SIT];
   {
     const uint4 *x4 = reinterpret_cast<const uint4 *>(x + (int64_t)t * D);
+    // every thread loads (clamped indices, surplus ignored): conditional
+    // loads would be waited for before the code stream is issued
 #pragma unroll
-    for (int it = 0; it < XIT; ++it) {
-      const int i = it * NT + tid;
-      xr[it] = (i < XU4) ? x4[i] : make_uint4(0, 0, 0, 0);
-    }
-    const char *sbp[4] = {resolve(pa, comp_index(PROJ_GATE, PART_S, NP), ref),
-                          resolve(pa, comp_index(PROJ_GATE, PART_B, NP), ref),
-                          resolve(pa, comp_index(PROJ_UP, PART_S, NP), ref),
-                          resolve(pa, comp_index(PROJ_UP, PART_B, NP), ref)};
+    for (int it = 0; it < XIT; ++it) xr[it] = load16(x4 + min(it * NT + tid, XU4 - 1));
+    // (selected by conditionals, not through an indexed array: a pointer
+    // picked out of a private array loses its global address space, and
+    // the flat load that results is waited for together with every load
+    // issued after it)
+    const char *gs = resolve(pa, comp_index(PROJ_GATE, PART_S, NP), ref);
+    const char *gb = resolve(pa, comp_index(PROJ_GATE, PART_B, NP), ref);
+    const char *us = resolve(pa, comp_index(PROJ_UP, PART_S, NP), ref);
+    const char *ub = resolve(pa, comp_index(PROJ_UP, PART_B, NP), ref);
 #pragma unroll
     for (int it = 0; it < SIT; ++it) {
-      const int i = it * NT + tid;
+      const int i = min(it * NT + tid, 4 * SB_U4 - 1);
       const int p = i / SB_U4, o = i % SB_U4;
-      sr[it] = (i < 4 * SB_U4)
-                   ? reinterpret_cast<const uint4 *>(sbp[p] + (int64_t)row0 * NG * 2)[o]
-                   : make_uint4(0, 0, 0, 0);
+      const char *sp = p == 0 ? gs : p == 1 ? gb : p == 2 ? us : ub;
+      sr[it] = load16(reinterpret_cast<const uint4 *>(sp + (int64_t)row0 * NG * 2) + o);
+    }
+  }
+  // the rows' projection biases, also ahead of the code stream
+  float gbv[RSTEPS], ubv[RSTEPS];
+#pragma unroll
+  for (int s = 0; s < RSTEPS; ++s) gbv[s] = ubv[s] = 0.f;
+  if (PBIAS) {
+    const uint16_t *gbias = reinterpret_cast<const uint16_t *>(
+        resolve(pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref));
+    const uint16_t *ubias = reinterpret_cast<const uint16_t *>(
+        resolve(pa, comp_index(PROJ_UP, PART_BIAS, NP), ref));
+#pragma unroll
+    for (int s = 0; s < RSTEPS; ++s) {
+      const int row = row0 + (wave * RSTEPS + s) * RPS + rsub;
+      gbv[s] = bf16_to_f32(gbias[row]);
+      ubv[s] = bf16_to_f32(ubias[row]);
     }
   }
 
-  // 2. every code load of this lane
+  // 2. every code load of this lane (the scheduling barriers keep the
+  //    small loads ahead of the code stream, and the staging behind it)
+  issue_order_fence();
   uint4 cg[RSTEPS][CPL], cu[RSTEPS][CPL];
 #pragma unroll
   for (int s = 0; s < RSTEPS; ++s) {
@@ -153,17 +173,13 @@ __global__ __launch_bounds__(WAVES * 64) void ffn_gate_up_kernel(
     const uint4 *g4 = reinterpret_cast<const uint4 *>(gw + (int64_t)row * (D / 2));
     const uint4 *u4 = reinterpret_cast<const uint4 *>(uw + (int64_t)row * (D / 2));
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int c = i * SG + j;
-      if (CPL * SG == U || c < U) {
-        cg[s][i] = load_stream16(g4 + c);
-        cu[s][i] = load_stream16(u4 + c);
-      } else {
-        cg[s][i] = make_uint4(0, 0, 0, 0);
-        cu[s][i] = make_uint4(0, 0, 0, 0);
-      }
+    for (int i = 0; i < CPL; ++i) {   // surplus chunks (c >= U) re-read the last one, unused
+      const int c = min(i * SG + j, U - 1);
+      cg[s][i] = load_stream16(g4 + c);
+      cu[s][i] = load_stream16(u4 + c);
     }
   }
+  issue_order_fence();
   // 3. stage scales/biases and the activations (pair order + chunk sums)
 #pragma unroll
   for (int it = 0; it < SIT; ++it) {
@@ -204,14 +220,8 @@ __global__ __launch_bounds__(WAVES * 64) void ffn_gate_up_kernel(
     pu = group_sum<SG>(pu);
     if (j == 0) {
       const int row = row0 + rl;
-      if (PBIAS) {
-        const uint16_t *gbias = reinterpret_cast<const uint16_t *>(
-            resolve(pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref));
-        const uint16_t *ubias = reinterpret_cast<const uint16_t *>(
-            resolve(pa, comp_index(PROJ_UP, PART_BIAS, NP), ref));
-        pg += bf16_to_f32(gbias[row]);
-        pu += bf16_to_f32(ubias[row]);
-      }
+      pg += gbv[s];   // 0 without projection bias
+      pu += ubv[s];
       h[(int64_t)pair * F + row] = (uint16_t)f32_to_bf16(apply_act(act, pg, pu, alpha, limit));
     }
   }
@@ -261,8 +271,9 @@ __global__ __launch_bounds__(64 * MOE_MAX_TOPK) void ffn_down_kernel(
   const int rb = blockIdx.x % WG_PER_TOK;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rsub = lane / SG, j = lane % SG;
-  const int pair = t * k + wave;
-  const int32_t ref = refs[pair];
+  // wave-uniform: the slot's addresses resolve in scalar registers
+  const int pair = __builtin_amdgcn_readfirstlane(t * k + wave);
+  const int32_t ref = __builtin_amdgcn_readfirstlane(refs[pair]);
   const float score = scores[pair];
   const int row0 = rb * ROWS_WG;
 
@@ -273,87 +284,81 @@ __global__ __launch_bounds__(64 * MOE_MAX_TOPK) void ffn_down_kernel(
   float *red = reinterpret_cast<float *>(reinterpret_cast<char *>(dyn_lds) +
                                          (size_t)k * LY::WAVE_BYTES);
 
-  const char *dw = resolve(pa, comp_index(PROJ_DOWN, PART_W, NP), ref);
-  uint4 cd[RSTEPS][CPL];
-  if (dw != nullptr) {
-    // small loads first (h of this expert, the rows' scales/biases), then
-    // the code stream; staging waits only for the former
-    constexpr int HIT = (HU4 + 63) / 64;
-    constexpr int SIT = (2 * SB_U4 + 63) / 64;
-    uint4 hr[HIT], sr[SIT];
-    const uint4 *h4 = reinterpret_cast<const uint4 *>(h + (int64_t)pair * F);
+  // an out-of-range ref reads slot 0, flags the error and contributes 0
+  bool ok;
+  const char *dw = resolve_safe(pa, comp_index(PROJ_DOWN, PART_W, NP), ref, ok);
+  const char *sp = resolve_safe(pa, comp_index(PROJ_DOWN, PART_S, NP), ref, ok);
+  const char *bp = resolve_safe(pa, comp_index(PROJ_DOWN, PART_B, NP), ref, ok);
+  if (!ok && lane == 0) flag_error();
+  // small loads first (h of this expert, the rows' scales/biases), then the
+  // code stream; staging then waits only for the former.  No branch around
+  // any load and every lane loads (indices clamped, surplus lanes ignored
+  // later): a conditional load would be waited for before the code stream.
+  constexpr int HIT = (HU4 + 63) / 64;
+  constexpr int SIT = (2 * SB_U4 + 63) / 64;
+  uint4 hr[HIT], sr[SIT], cd[RSTEPS][CPL];
+  const uint4 *h4 = reinterpret_cast<const uint4 *>(h + (int64_t)pair * F);
 #pragma unroll
-    for (int it = 0; it < HIT; ++it) {
-      const int i = it * 64 + lane;
-      hr[it] = (i < HU4) ? h4[i] : make_uint4(0, 0, 0, 0);
-    }
-    const char *sp = resolve(pa, comp_index(PROJ_DOWN, PART_S, NP), ref);
-    const char *bp = resolve(pa, comp_index(PROJ_DOWN, PART_B, NP), ref);
+  for (int it = 0; it < HIT; ++it) hr[it] = load16(h4 + min(it * 64 + lane, HU4 - 1));
 #pragma unroll
-    for (int it = 0; it < SIT; ++it) {
-      const int i = it * 64 + lane;
-      const int p = i / SB_U4, o = i % SB_U4;
-      sr[it] = (i < 2 * SB_U4)
-                   ? reinterpret_cast<const uint4 *>((p ? bp : sp) + (int64_t)row0 * NG * 2)[o]
-                   : make_uint4(0, 0, 0, 0);
-    }
+  for (int it = 0; it < SIT; ++it) {
+    const int i = min(it * 64 + lane, 2 * SB_U4 - 1);
+    const int p = i / SB_U4, o = i % SB_U4;
+    sr[it] = load16(reinterpret_cast<const uint4 *>((p ? bp : sp) + (int64_t)row0 * NG * 2) + o);
+  }
+  float dbv[RSTEPS];
 #pragma unroll
-    for (int s = 0; s < RSTEPS; ++s) {
-      const int row = row0 + s * RPS + rsub;
-      const uint4 *d4 = reinterpret_cast<const uint4 *>(dw + (int64_t)row * (F / 2));
+  for (int s = 0; s < RSTEPS; ++s) dbv[s] = 0.f;
+  if (PBIAS) {
+    bool okb;
+    const uint16_t *dbias = reinterpret_cast<const uint16_t *>(
+        resolve_safe(pa, comp_index(PROJ_DOWN, PART_BIAS, NP), ref, okb));
 #pragma unroll
-      for (int i = 0; i < CPL; ++i) {
-        const int c = i * SG + j;
-        cd[s][i] = (CPL * SG == U || c < U) ? load_stream16(d4 + c) : make_uint4(0, 0, 0, 0);
-      }
-    }
+    for (int s = 0; s < RSTEPS; ++s) dbv[s] = bf16_to_f32(dbias[row0 + s * RPS + rsub]);
+  }
+  issue_order_fence();
 #pragma unroll
-    for (int it = 0; it < SIT; ++it) {
-      const int i = it * 64 + lane;
-      if (i < 2 * SB_U4) sb_l[i] = sr[it];
-    }
+  for (int s = 0; s < RSTEPS; ++s) {
+    const int row = row0 + s * RPS + rsub;
+    const uint4 *d4 = reinterpret_cast<const uint4 *>(dw + (int64_t)row * (F / 2));
 #pragma unroll
-    for (int it = 0; it < HIT; ++it) {
-      const int i = it * 64 + lane;
-      float s = 0.f;
-      if (i < HU4) s = stage_piece<U>(act_l, i, hr[it]);
-      s += dpp_f<kDppQuadXor1>(s);
-      s += dpp_f<kDppQuadXor2>(s);
-      if (i < HU4 && (i & 3) == 0) asum_l[i >> 2] = s;
-    }
-  } else if (lane == 0) {
-    flag_error();
+    for (int i = 0; i < CPL; ++i)   // surplus chunks (c >= U) re-read the last one, unused
+      cd[s][i] = load_stream16(d4 + min(i * SG + j, U - 1));
+  }
+  issue_order_fence();
+#pragma unroll
+  for (int it = 0; it < SIT; ++it) {
+    const int i = it * 64 + lane;
+    if (i < 2 * SB_U4) sb_l[i] = sr[it];
+  }
+#pragma unroll
+  for (int it = 0; it < HIT; ++it) {
+    const int i = it * 64 + lane;
+    float s = 0.f;
+    if (i < HU4) s = stage_piece<U>(act_l, i, hr[it]);
+    s += dpp_f<kDppQuadXor1>(s);
+    s += dpp_f<kDppQuadXor2>(s);
+    if (i < HU4 && (i & 3) == 0) asum_l[i >> 2] = s;
   }
   __syncthreads();
 
-  if (dw != nullptr) {
-    const uint16_t *sbh = reinterpret_cast<const uint16_t *>(sb_l);
-    constexpr int SBN = SB_U4 * 8;
+  const uint16_t *sbh = reinterpret_cast<const uint16_t *>(sb_l);
+  constexpr int SBN = SB_U4 * 8;
 #pragma unroll
-    for (int s = 0; s < RSTEPS; ++s) {
-      const int rl = s * RPS + rsub;
-      float p = 0.f;
+  for (int s = 0; s < RSTEPS; ++s) {
+    const int rl = s * RPS + rsub;
+    float p = 0.f;
 #pragma unroll
-      for (int i = 0; i < CPL; ++i) {
-        const int c = i * SG + j;
-        if (CPL * SG == U || c < U) {
-          const int g = rl * NG + (c >> 1);
-          const float Sd = bf16_to_f32(sbh[g]), Bd = bf16_to_f32(sbh[SBN + g]);
-          p += Sd * chunk_dot_lds<U>(cd[s][i], act_l, c) + (Bd - 128.f * Sd) * asum_l[c];
-        }
-      }
-      p = group_sum<SG>(p);
-      if (j == 0) {
-        if (PBIAS) {
-          const uint16_t *dbias = reinterpret_cast<const uint16_t *>(
-              resolve(pa, comp_index(PROJ_DOWN, PART_BIAS, NP), ref));
-          p += bf16_to_f32(dbias[row0 + rl]);
-        }
-        red[wave * ROWS_WG + rl] = score * p;
+    for (int i = 0; i < CPL; ++i) {
+      const int c = i * SG + j;
+      if (CPL * SG == U || c < U) {
+        const int g = rl * NG + (c >> 1);
+        const float Sd = bf16_to_f32(sbh[g]), Bd = bf16_to_f32(sbh[SBN + g]);
+        p += Sd * chunk_dot_lds<U>(cd[s][i], act_l, c) + (Bd - 128.f * Sd) * asum_l[c];
       }
     }
-  } else {
-    for (int i = lane; i < ROWS_WG; i += 64) red[wave * ROWS_WG + i] = 0.f;
+    p = group_sum<SG>(p);
+    if (j == 0) red[wave * ROWS_WG + rl] = ok ? score * (p + dbv[s]) : 0.f;
   }
   __syncthreads();
   for (int r = threadIdx.x; r < ROWS_WG; r += blockDim.x) {

@@ -99,7 +99,9 @@ def test_prefill_through_the_block(world):
     """T = 40 tokens in one call (the prefill path: many-token router, np.unique
     + inverse index build, grouped MFMA block) against the batched oracle."""
     geom, store, W, _, host = world
-    pool = ExpertPool(geom, 200, store, n_layers=L)
+    # room for layer 1's experts and the lookahead's prefetch of layer 2
+    # (each up to all 128 over 40 tokens), both issued before the acquire
+    pool = ExpertPool(geom, 300, store, n_layers=L)
     blocks = _blocks(geom, pool, W)
     xs = synth.hidden_states(40, L, geom.d_model, "cuda", 20260504)
     x = xs[:, 1].contiguous()                     # 40 tokens at layer 1
