@@ -137,13 +137,9 @@ __device__ __forceinline__ float ld_dev(const float *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// All threads of the workgroup: wait until the counter's sum >= target.
-// Wave 0 polls the sub-counters (device scope); the barrier then releases
-// the workgroup, whose later device-scope loads observe every store that was
-// complete before the arrivals counted.  Bounded: past the spin limit, or as
-// soon as any workgroup has flagged an error, it gives up (wrong results,
-// never a hang).
 // One whole wave: poll until the counter's sum >= target (no barrier).
+// Bounded: past the spin limit, or as soon as any workgroup has flagged an
+// error, it gives up (wrong results, never a hang).
 __device__ __forceinline__ void wave_wait(const uint32_t *c, uint32_t target) {
   const int lane = threadIdx.x & 63;
   uint32_t spins = 0;
@@ -165,8 +161,12 @@ __device__ __forceinline__ void wave_wait(const uint32_t *c, uint32_t target) {
   }
 }
 
-__device__ __forceinline__ void wg_wait(const uint32_t *c, uint32_t target) {
-  if (threadIdx.x < 64) wave_wait(c, target);
+// All threads of the workgroup: wait until the counter's sum >= target.
+// Wave `poll_wave` polls the sub-counters (device scope); the barrier then
+// releases the workgroup, whose later device-scope loads observe every store
+// that was complete before the arrivals counted.
+__device__ __forceinline__ void wg_wait(const uint32_t *c, uint32_t target, int poll_wave) {
+  if ((threadIdx.x >> 6) == poll_wave) wave_wait(c, target);
   __syncthreads();
 }
 
@@ -282,17 +282,24 @@ __device__ __forceinline__ void u_load(const StackArgs &a, int32_t ref, int row0
   constexpr int D = C::D_, NG = C::NG, SGU = C::SGU, CPLU = C::CPLU, RPSU = C::RPSU;
   constexpr int SB_U4 = C::SB_U4, NP = C::NP, NT = C::NT;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const char *gw = resolve(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref);
-  if (gw == nullptr) return;
-  const char *uw = resolve(a.pa, comp_index(PROJ_UP, PART_W, NP), ref);
+  // No branch around any load and no conditional load (either makes the
+  // compiler wait for the loads before it): an out-of-range ref reads slot 0
+  // (the phase that consumes the registers flags it), surplus lanes load a
+  // clamped index.
+  ref = __builtin_amdgcn_readfirstlane(ref);
+  bool ok;
+  const char *gw = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
+  const char *uw = resolve_safe(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
+  const char *sb[4] = {resolve_safe(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok),
+                       resolve_safe(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok),
+                       resolve_safe(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok),
+                       resolve_safe(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok)};
 #pragma unroll
   for (int it = 0; it < C::SIT; ++it) {
-    const int i = it * NT + tid;
+    const int i = min(it * NT + tid, 4 * SB_U4 - 1);
     const int p = i / SB_U4, o = i % SB_U4;
-    const int part = (p & 1) ? PART_B : PART_S, proj = (p >> 1) ? PROJ_UP : PROJ_GATE;
-    const char *sp = resolve(a.pa, comp_index(proj, part, NP), ref);
-    sr[it] = (i < 4 * SB_U4) ? reinterpret_cast<const uint4 *>(sp + (int64_t)row0 * NG * 2)[o]
-                             : make_uint4(0, 0, 0, 0);
+    const char *sp = p == 0 ? sb[0] : p == 1 ? sb[1] : p == 2 ? sb[2] : sb[3];
+    sr[it] = load16(reinterpret_cast<const uint4 *>(sp + (int64_t)row0 * NG * 2) + o);
   }
   if (wave < C::WAVES_U) {
     const int uj = lane % SGU, usub = lane / SGU;
@@ -314,23 +321,23 @@ __device__ __forceinline__ void d_load(const StackArgs &a, int32_t ref, int drow
   constexpr int F = C::F_, NGF = C::NGF, SGD = C::SGD, CPLD = C::CPLD, UF = C::UF;
   constexpr int SBD_U4 = C::SBD_U4, NP = C::NP;
   const int lane = threadIdx.x & 63;
-  const char *dw = resolve(a.pa, comp_index(PROJ_DOWN, PART_W, NP), ref);
-  if (dw == nullptr) return;
+  // (unconditional loads, as in u_load)
+  ref = __builtin_amdgcn_readfirstlane(ref);
+  bool ok;
+  const char *dw = resolve_safe(a.pa, comp_index(PROJ_DOWN, PART_W, NP), ref, ok);
+  const char *ds = resolve_safe(a.pa, comp_index(PROJ_DOWN, PART_S, NP), ref, ok);
+  const char *db = resolve_safe(a.pa, comp_index(PROJ_DOWN, PART_B, NP), ref, ok);
 #pragma unroll
   for (int it = 0; it < C::SDIT; ++it) {
-    const int i = it * 64 + lane;
+    const int i = min(it * 64 + lane, 2 * SBD_U4 - 1);
     const int p = i / SBD_U4, o = i % SBD_U4;
-    const char *sp = resolve(a.pa, comp_index(PROJ_DOWN, p ? PART_B : PART_S, NP), ref);
-    sdr[it] = (i < 2 * SBD_U4) ? reinterpret_cast<const uint4 *>(sp + (int64_t)drow0 * NGF * 2)[o]
-                               : make_uint4(0, 0, 0, 0);
+    sdr[it] = load16(reinterpret_cast<const uint4 *>((p ? db : ds) + (int64_t)drow0 * NGF * 2) + o);
   }
   const int dj = lane % SGD, dsub = lane / SGD;
   const uint4 *d4 = reinterpret_cast<const uint4 *>(dw + (int64_t)(drow0 + dsub) * (F / 2));
 #pragma unroll
-  for (int i = 0; i < CPLD; ++i) {
-    const int c = i * SGD + dj;
-    cd[i] = (CPLD * SGD == UF || c < UF) ? load_stream16(d4 + c) : make_uint4(0, 0, 0, 0);
-  }
+  for (int i = 0; i < CPLD; ++i)   // surplus chunks (c >= UF) re-read the last one, unused
+    cd[i] = load_stream16(d4 + min(i * SGD + dj, UF - 1));
 }
 
 template <int D, int F, int K, bool PBIAS>
@@ -358,6 +365,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
   __shared__ float sel_sc[K];
   __shared__ int32_t sel_ref[K];
   __shared__ int pred_buf[2][K];     // lookahead's K best, rank order (slot l & 1)
+  __shared__ int32_t pred_ref[2][K]; // their slot refs (looked up by the ranking wave)
   __shared__ int pred_cnt[2];
   __shared__ int d_rank[K];          // D wave w: routing rank of its expert
   __shared__ int d_fix[K];           // D wave w: fix-up slot, or -1 (predicted at w)
@@ -410,11 +418,16 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       }
     }
     // ------------------------------------------------------ layer start ----
-    if (l > 0) wg_wait(counter(a, l - 1, CNT_D), ep * C::ITEMS_D);
+    // polled by the ranking wave: the one wave with no staging loads in
+    // flight here (loads complete in order, so a poll issued behind staging
+    // loads would return only after them); it issues its own down staging
+    // right after
+    if (l > 0) wg_wait(counter(a, l - 1, CNT_D), ep * C::ITEMS_D, W_RANK);
     else __syncthreads();
     if (wave == 0) trace_mark(a, l, TR_R_WAITED);
     const int pcnt = pred_cnt[l & 1];
     const int *P = pred_buf[l & 1];
+    if (wave == W_RANK && W_RANK < pcnt) d_load<C>(a, pred_ref[l & 1][W_RANK], drow0, cd, sdr);
     // ------------------------------------------------------- role split ----
     if (wave < W_ROUTER) {
       // stage x_l (pair order + 32-input sums) and the predicted block's
@@ -441,7 +454,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
       // gate/up of the predicted expert at this workgroup's position
       if (wave < C::WAVES_U && upos < pcnt)
-        u_rows<C>(a, tab[P[upos]], urow0, cg, cu, act_l, asum_l, sbu_l,
+        u_rows<C>(a, pred_ref[l & 1][upos], urow0, cg, cu, act_l, asum_l, sbu_l,
                   h_pred + (size_t)upos * F);
       // the position's counter advances by NPOS every layer, work or not
       __builtin_amdgcn_s_waitcnt(0);
@@ -491,8 +504,16 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
           if (s1) a.pred[(size_t)l * a.kp + r1] = e1;
         }
         int *pn = pred_buf[(l + 1) & 1];
-        if (s0 && r0 < K) pn[r0] = e0;
-        if (s1 && r1 < K) pn[r1] = e1;
+        int32_t *pr = pred_ref[(l + 1) & 1];
+        const int32_t *tabn = a.table + (size_t)(l + 1) * a.E;
+        if (s0 && r0 < K) {
+          pn[r0] = e0;
+          pr[r0] = tabn[e0];
+        }
+        if (s1 && r1 < K) {
+          pn[r1] = e1;
+          pr[r1] = tabn[e1];
+        }
         if (lane == 0) pred_cnt[(l + 1) & 1] = min(a.kp, K);
       }
     } else {
@@ -683,12 +704,12 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
     wg_arrive(counter(a, l, CNT_D));
     if (wave == 0) trace_mark(a, l, TR_D_ARRIVED);
     // ----------------------------- staging loads of layer l+1's prediction
+    // (the ranking wave's down rows are staged after the next layer's wait)
     if (has_next) {
       const int pc = pred_cnt[(l + 1) & 1];
-      const int *Pn = pred_buf[(l + 1) & 1];
-      const int32_t *tabn = a.table + (size_t)(l + 1) * a.E;
-      if (upos < pc) u_load<C>(a, tabn[Pn[upos]], urow0, cg, cu, sr);
-      if (wave < K && wave < pc) d_load<C>(a, tabn[Pn[wave]], drow0, cd, sdr);
+      const int32_t *Rn = pred_ref[(l + 1) & 1];
+      if (upos < pc) u_load<C>(a, Rn[upos], urow0, cg, cu, sr);
+      if (wave < K && wave != W_RANK && wave < pc) d_load<C>(a, Rn[wave], drow0, cd, sdr);
     }
   }
 }
