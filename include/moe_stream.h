@@ -190,8 +190,10 @@ int moe_route(const uint16_t *x, int32_t T, int32_t d_model,
  * moe_ffn_decode per layer on one stream, with the layer's phases chained by
  * device-side counters instead of kernel boundaries, and layer l+1 starting
  * only after y[l] is complete.
- * epoch: 1 for the first launch on a zeroed workspace, then 2, 3, ...; after
- * MOE_ERR_DEVICE the workspace must be zeroed and the epoch restarted.
+ * epoch: 1 for the first launch on a zeroed workspace, then 2, 3, ... while
+ * (epoch + 1) * n_layers < 2^32 (past that, MOE_ERR_INVALID); after
+ * MOE_ERR_DEVICE, or to go past that bound, zero the workspace and restart
+ * at 1.  A workspace serves one stack (one n_layers) at a time.
  * This fuses the per-layer calls of streaming_call (engine_v3.py:493-609) for
  * a device-resident pool; it has no single counterpart in the reference.
  */

@@ -338,9 +338,10 @@ int moe_stack_trace(void *device_buf, size_t bytes) {
 size_t moe_stack_workspace(const moe_geom *g, int32_t n_layers, int32_t E, int32_t k) {
   if (!g || n_layers <= 0 || E <= 0 || k <= 0) return 0;
   const size_t counters = (size_t)n_layers * moe::kCountersPerLayer * moe::kCounterWords * 4;
-  const size_t logits = ((size_t)2 * E * 4 + 255) & ~(size_t)255;
-  const size_t h = ((size_t)2 * k * g->d_ff * 2 + 255) & ~(size_t)255;   // bf16: predicted, fix-up
-  return counters + logits + h;
+  const size_t logits = ((size_t)2 * E * 8 + 255) & ~(size_t)255;   // flagged entries
+  const size_t h = ((size_t)k * g->d_ff * 2 + 255) & ~(size_t)255;      // bf16, predicted
+  const size_t hfix = ((size_t)k * (g->d_ff / 2) * 8 + 255) & ~(size_t)255;   // flagged fix-up
+  return counters + logits + h + hfix;
 }
 
 int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_layers,
@@ -376,6 +377,9 @@ int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_lay
     return fail(MOE_ERR_INVALID, "workspace %zu < %zu bytes", workspace_bytes,
                 moe_stack_workspace(g, n_layers, E, k));
   if (epoch == 0) return fail(MOE_ERR_INVALID, "epoch must start at 1");
+  if ((uint64_t)epoch * (uint64_t)n_layers + (uint64_t)n_layers > 0xffffffffull)
+    return fail(MOE_ERR_INVALID, "epoch %u too large for %d layers: zero the workspace and "
+                "restart at 1", epoch, n_layers);
   char *ws = static_cast<char *>(workspace);
   moe::StackArgs a;
   a.pa = pa;
@@ -391,9 +395,11 @@ int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_lay
   a.miss = miss_count;
   a.cnt = reinterpret_cast<uint32_t *>(ws);
   ws += (size_t)n_layers * moe::kCountersPerLayer * moe::kCounterWords * 4;
-  a.logits = reinterpret_cast<float *>(ws);
-  ws += ((size_t)2 * E * 4 + 255) & ~(size_t)255;
+  a.lgt = reinterpret_cast<uint64_t *>(ws);
+  ws += ((size_t)2 * E * 8 + 255) & ~(size_t)255;
   a.h = reinterpret_cast<uint16_t *>(ws);
+  ws += ((size_t)k * g->d_ff * 2 + 255) & ~(size_t)255;
+  a.hfix = reinterpret_cast<uint64_t *>(ws);
   a.L = n_layers;
   a.E = E;
   a.kp = k_pred;

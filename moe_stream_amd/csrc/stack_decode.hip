@@ -56,8 +56,9 @@ struct StackArgs {
   int32_t *refs_out;      // [L][K]
   int32_t *pred;          // [L][KP]
   int32_t *miss;          // [L]
-  float *logits;          // ws [2][E]
-  uint16_t *h;            // ws [2][K][F] bf16 activations: predicted, fix-up
+  uint64_t *lgt;          // ws [2][E] router / lookahead logits, flagged (put_logit)
+  uint16_t *h;            // ws [K][F] bf16 activations of the predicted experts
+  uint64_t *hfix;         // ws [K][F/2] fix-up activations: 2 bf16 + 32-bit flag each
   uint32_t *cnt;          // ws [L][3][kSub] counters, 128 B apart
   int L, E, kp, mode, renorm, act;
   float alpha, limit;
@@ -94,9 +95,26 @@ constexpr int kSub = 8;
 constexpr int kCounterWords = kSub * 32;
 
 // Counters of one layer: router rows, lookahead rows, the layer output, one
-// per predicted position for its activations, one per fix-up slot.
-enum { CNT_R = 0, CNT_RL = 1, CNT_D = 2, CNT_U0 = 3, CNT_F0 = 11 };
-constexpr int kCountersPerLayer = CNT_F0 + 8;
+// per predicted position for its activations.  (Fix-up activations carry
+// their own flags instead.)
+enum { CNT_D = 0, CNT_U0 = 1 };
+constexpr int kCountersPerLayer = CNT_U0 + 8;
+
+// The flag a data entry exchanged between workgroups carries (router logits,
+// fix-up activations): unique per (token, layer), so an entry left by an
+// earlier token or layer never passes for a current one.
+__device__ __forceinline__ uint32_t layer_flag(const StackArgs &a, int l) {
+  return a.epoch * (uint32_t)a.L + (uint32_t)l;
+}
+
+// Router logits cross workgroups as flagged 8-byte entries, the fp32 logit in
+// the low word and the layer flag in the high word: one device-scope store
+// publishes a logit, and readers poll the entries themselves (no counter to
+// arrive on, no load after the wait).
+__device__ __forceinline__ void put_logit(uint64_t *slot, float v, uint32_t fl) {
+  __hip_atomic_store(slot, (uint64_t)__float_as_uint(v) | ((uint64_t)fl << 32),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 __device__ __forceinline__ uint32_t *counter(const StackArgs &a, int l, int which) {
   return a.cnt + ((size_t)l * kCountersPerLayer + which) * kCounterWords;
@@ -128,15 +146,6 @@ __device__ __forceinline__ uint4 ld_dev16(const float *p) {
   return r;
 }
 
-// Data crossing workgroups (logits, h) moves through device-scope accesses
-// (sc1: coherent across the XCDs without an L2 writeback or invalidate).
-__device__ __forceinline__ void st_dev(float *p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_dev(const float *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // One whole wave: poll until the counter's sum >= target (no barrier).
 // Bounded: past the spin limit, or as soon as any workgroup has flagged an
 // error, it gives up (wrong results, never a hang).
@@ -152,6 +161,30 @@ __device__ __forceinline__ void wave_wait(const uint32_t *c, uint32_t target) {
     v += dpp_i<kDppHalfMirror>(v);
     const uint32_t sum = (uint32_t)__builtin_amdgcn_readfirstlane(v);
     if (sum >= target) break;
+    __builtin_amdgcn_s_sleep(1);
+    if (++spins > kSpinLimit ||
+        __hip_atomic_load(&g_device_error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+      if (lane == 0) flag_error();
+      break;
+    }
+  }
+}
+
+// One whole wave: the logits of entries lane and lane + 64 of `slots` (n
+// entries, n <= 128), polled until every present entry carries `fl`.
+// Bounded like wave_wait.
+__device__ __forceinline__ void get_logits(const uint64_t *slots, int n, uint32_t fl, float &z0,
+                                           float &z1) {
+  const int lane = threadIdx.x & 63, e0 = lane, e1 = lane + 64;
+  const uint64_t *p0 = slots + min(e0, n - 1), *p1 = slots + min(e1, n - 1);
+  uint32_t spins = 0;
+  while (true) {
+    const uint64_t v0 = __hip_atomic_load(p0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t v1 = __hip_atomic_load(p1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool ok = (e0 >= n || (uint32_t)(v0 >> 32) == fl) && (e1 >= n || (uint32_t)(v1 >> 32) == fl);
+    z0 = __uint_as_float((uint32_t)v0);
+    z1 = __uint_as_float((uint32_t)v1);
+    if (__ballot(!ok) == 0) break;
     __builtin_amdgcn_s_sleep(1);
     if (++spins > kSpinLimit ||
         __hip_atomic_load(&g_device_error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
@@ -273,6 +306,114 @@ __device__ __forceinline__ void u_rows(const StackArgs &a, int32_t ref, int row0
   }
 }
 
+// One fix-up task, one whole wave: gate/up + activation of rows
+// [4b, 4b+4) of a routed expert that was not predicted (16 lanes per row, as
+// in u_rows), straight from the pool; its 4 activations go out as two
+// flagged 8-byte entries (2 bf16 + fix_flag) of `hf`, the expert's [F/2]
+// entries.  `sbw`: this wave's 64 uint4 of LDS for the rows' scales.
+template <class C>
+__device__ __forceinline__ void fix_task(const StackArgs &a, int32_t ref, int b,
+                                         const uint4 *act_l, const float *asum_l, uint4 *sbw,
+                                         uint64_t *hf, uint32_t fl) {
+  constexpr int D = C::D_, U = C::U, NG = C::NG, SGU = C::SGU, CPLU = C::CPLU, NP = C::NP;
+  static_assert(C::RPSU == 4 && SGU == 16 && NG * 2 * 4 == 16 * 16,
+                "a task: 4 rows of 16 lanes; its scales: 4 arrays of 16 pieces");
+  const int lane = threadIdx.x & 63, uj = lane % SGU, usub = lane / SGU;
+  ref = __builtin_amdgcn_readfirstlane(ref);
+  bool ok;
+  const char *gw = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
+  const char *uw = resolve_safe(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
+  const char *gs = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok);
+  const char *gb = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok);
+  const char *us = resolve_safe(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok);
+  const char *ub = resolve_safe(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok);
+  const int row = 4 * b + usub;
+  // small loads first: lane -> scale array lane / 16, piece lane % 16 of the
+  // rows' 256-byte block; the projection biases of its row
+  const int arr = lane >> 4;
+  const char *sa = arr == 0 ? gs : arr == 1 ? gb : arr == 2 ? us : ub;
+  const uint4 sv = load16(reinterpret_cast<const uint4 *>(sa + (int64_t)(4 * b) * NG * 2) + (lane & 15));
+  float gbv = 0.f, ubv = 0.f;
+  if (C::PBIAS_) {
+    bool okb;
+    gbv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
+        resolve_safe(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[row]);
+    ubv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
+        resolve_safe(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[row]);
+  }
+  issue_order_fence();
+  uint4 cg[CPLU], cu[CPLU];
+  const uint4 *g4 = reinterpret_cast<const uint4 *>(gw + (int64_t)row * (D / 2));
+  const uint4 *u4 = reinterpret_cast<const uint4 *>(uw + (int64_t)row * (D / 2));
+#pragma unroll
+  for (int i = 0; i < CPLU; ++i) {
+    cg[i] = load_stream16(g4 + i * SGU + uj);
+    cu[i] = load_stream16(u4 + i * SGU + uj);
+  }
+  issue_order_fence();
+  sbw[lane] = sv;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_wave_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  const uint16_t *sbh = reinterpret_cast<const uint16_t *>(sbw);
+  constexpr int SBN = 4 * NG;   // bf16 per array: 4 rows x NG groups
+  float pg = 0.f, pu = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPLU; ++i) {
+    const int c = i * SGU + uj;
+    const int g = usub * NG + (c >> 1);
+    const float Sg = bf16_to_f32(sbh[g]), Bg = bf16_to_f32(sbh[SBN + g]);
+    const float Su = bf16_to_f32(sbh[2 * SBN + g]), Bu = bf16_to_f32(sbh[3 * SBN + g]);
+    const float xs = asum_l[c];
+    pg += Sg * chunk_dot_lds<U>(cg[i], act_l, c) + (Bg - 128.f * Sg) * xs;
+    pu += Su * chunk_dot_lds<U>(cu[i], act_l, c) + (Bu - 128.f * Su) * xs;
+  }
+  pg = group_sum<SGU>(pg) + gbv;
+  pu = group_sum<SGU>(pu) + ubv;
+  uint32_t hb = 0;
+  if (ok) hb = f32_to_bf16(apply_act(a.act, pg, pu, a.alpha, a.limit));
+  else if (lane == 0) flag_error();
+  const uint32_t h0 = __builtin_amdgcn_readlane(hb, 0), h1 = __builtin_amdgcn_readlane(hb, 16);
+  const uint32_t h2 = __builtin_amdgcn_readlane(hb, 32), h3 = __builtin_amdgcn_readlane(hb, 48);
+  if (lane == 0) {
+    const uint64_t f = (uint64_t)fl << 32;
+    __hip_atomic_store(hf + 2 * b, (uint64_t)(h0 | (h1 << 16)) | f, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(hf + 2 * b + 1, (uint64_t)(h2 | (h3 << 16)) | f, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// One whole wave: the F activations of fix-up slot `hf` as two 16-byte pieces
+// per lane (pieces lane and lane + 64, 8 bf16 each), polled until every entry
+// carries the flag `fl`.  Bounded like wave_wait.
+template <int HU4>
+__device__ __forceinline__ void fix_acts(const uint64_t *hf, uint32_t fl, uint4 &p0, uint4 &p1) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t *e0 = hf + 4 * min(lane, HU4 - 1), *e1 = hf + 4 * min(lane + 64, HU4 - 1);
+  uint32_t spins = 0;
+  while (true) {
+    uint64_t v[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      v[q] = __hip_atomic_load(e0 + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      v[4 + q] = __hip_atomic_load(e1 + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    bool ok = true;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) ok = ok && (uint32_t)(v[q] >> 32) == fl;
+    p0 = make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+    p1 = make_uint4((uint32_t)v[4], (uint32_t)v[5], (uint32_t)v[6], (uint32_t)v[7]);
+    if (__ballot(!ok) == 0) break;
+    __builtin_amdgcn_s_sleep(1);
+    if (++spins > kSpinLimit ||
+        __hip_atomic_load(&g_device_error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+      if (lane == 0) flag_error();
+      break;
+    }
+  }
+}
+
 // Register loads of one workgroup's gate/up block (waves 0..WAVES_U-1: the
 // codes of its rows; every thread: its share of the block's scales).
 template <class C>
@@ -380,7 +521,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
   const int upos = wg / NPOS, urow0 = (wg % NPOS) * ROWS_U;   // gate/up block
   const int drow0 = wg * ROWS_D;                               // down block
   const int dj = lane % SGD, dsub = lane / SGD;
-  uint16_t *h_pred = a.h, *h_fix = a.h + (size_t)K * F;
+  uint16_t *h_pred = a.h;
   if (tid < 2) {
     pred_cnt[tid] = 0;               // layer 0 has no prediction
     u_done[tid] = 0;
@@ -483,18 +624,21 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
           acc = dot2_bf16(wr[it].w, v[it].w, acc);
         }
         acc = group_sum<64>(acc);
-        if (lane == 0) st_dev(a.logits + (rnxt ? a.E : 0) + e, acc);
-        wave_arrive(counter(a, l, rnxt ? CNT_RL : CNT_R));
+        if (lane == 0) put_logit(a.lgt + (rnxt ? a.E : 0) + e, acc, layer_flag(a, l));
         trace_mark(a, l, TR_R_ARRIVED);
       }
       // lookahead ranking of layer l+1: raw bf16 logits of its router on x_l
       if (has_next) {
-        wave_wait(counter(a, l, CNT_RL), ep * a.E);
         const int e0 = lane, e1 = lane + 64;
         const uint16_t *bias = a.bias ? a.bias + (size_t)(l + 1) * a.E : nullptr;
-        float z0 = -INFINITY, z1 = -INFINITY;
-        if (e0 < a.E) z0 = round_bf16(ld_dev(a.logits + a.E + e0) + (bias ? bf16_to_f32(bias[e0]) : 0.f));
-        if (e1 < a.E) z1 = round_bf16(ld_dev(a.logits + a.E + e1) + (bias ? bf16_to_f32(bias[e1]) : 0.f));
+        const float b0 = bias ? bf16_to_f32(bias[min(e0, a.E - 1)]) : 0.f;   // before the wait
+        const float b1 = bias ? bf16_to_f32(bias[min(e1, a.E - 1)]) : 0.f;
+        const int32_t *tabn = a.table + (size_t)(l + 1) * a.E;
+        const int32_t t0 = tabn[min(e0, a.E - 1)], t1 = tabn[min(e1, a.E - 1)];
+        float l0, l1;
+        get_logits(a.lgt + a.E, a.E, layer_flag(a, l), l0, l1);
+        const float z0 = e0 < a.E ? round_bf16(l0 + b0) : -INFINITY;
+        const float z1 = e1 < a.E ? round_bf16(l1 + b1) : -INFINITY;
         bool s0, s1;
         int r0, r1;
         select_topk(e0 < a.E ? order_key(z0) : -1, e1 < a.E ? order_key(z1) : -1, a.kp, lane,
@@ -505,14 +649,13 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
         }
         int *pn = pred_buf[(l + 1) & 1];
         int32_t *pr = pred_ref[(l + 1) & 1];
-        const int32_t *tabn = a.table + (size_t)(l + 1) * a.E;
         if (s0 && r0 < K) {
           pn[r0] = e0;
-          pr[r0] = tabn[e0];
+          pr[r0] = t0;
         }
         if (s1 && r1 < K) {
           pn[r1] = e1;
-          pr[r1] = tabn[e1];
+          pr[r1] = t1;
         }
         if (lane == 0) pred_cnt[(l + 1) & 1] = min(a.kp, K);
       }
@@ -520,13 +663,15 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       // ---- routing: every workgroup ranks this layer's logits ----------
       const int e0 = lane, e1 = lane + 64;
       const uint16_t *bias = a.bias ? a.bias + (size_t)l * a.E : nullptr;
-      const float b0 = (bias && e0 < a.E) ? bf16_to_f32(bias[e0]) : 0.f;   // before the wait
-      const float b1 = (bias && e1 < a.E) ? bf16_to_f32(bias[e1]) : 0.f;
-      wave_wait(counter(a, l, CNT_R), ep * a.E);
+      const float b0 = bias ? bf16_to_f32(bias[min(e0, a.E - 1)]) : 0.f;   // before the wait
+      const float b1 = bias ? bf16_to_f32(bias[min(e1, a.E - 1)]) : 0.f;
+      // every expert's slot ref, also before the wait (clamped, unconditional)
+      const int32_t t0 = tab[min(e0, a.E - 1)], t1 = tab[min(e1, a.E - 1)];
+      float l0, l1;
+      get_logits(a.lgt, a.E, layer_flag(a, l), l0, l1);
       trace_mark(a, l, TR_R_ALL);
-      float z0 = -INFINITY, z1 = -INFINITY;
-      if (e0 < a.E) z0 = round_bf16(ld_dev(a.logits + e0) + b0);
-      if (e1 < a.E) z1 = round_bf16(ld_dev(a.logits + e1) + b1);
+      const float z0 = e0 < a.E ? round_bf16(l0 + b0) : -INFINITY;
+      const float z1 = e1 < a.E ? round_bf16(l1 + b1) : -INFINITY;
       trace_mark_after(a, l, TR_LOGITS, z0 + z1);
       float v0 = z0, v1 = z1;
       if (a.mode == MOE_ROUTE_SOFTMAX_TOPK) {
@@ -561,12 +706,12 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       if (s0) {
         sel_id[r0] = e0;
         sel_sc[r0] = sc0;
-        sel_ref[r0] = tab[e0];
+        sel_ref[r0] = t0;
       }
       if (s1) {
         sel_id[r1] = e1;
         sel_sc[r1] = sc1;
-        sel_ref[r1] = tab[e1];
+        sel_ref[r1] = t1;
       }
       // ---- which D wave takes which routed expert -----------------------
       // Predicted position w keeps its expert if it was routed (its codes
@@ -616,31 +761,36 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       a.refs_out[(size_t)l * K + tid] = sel_ref[tid];
       if (sel_ref[tid] < 0) atomicAdd(a.miss + l, 1);
     }
+    // down rows of a routed expert that was not predicted: loaded now, so
+    // their latency overlaps the fix-up pass
+    int d_r = 0, d_fx = -1;
+    int32_t d_ref = 0;
+    if (wave < K) {
+      d_r = d_rank[wave];
+      d_fx = d_fix[wave];
+      d_ref = sel_ref[d_r];
+      if (d_fx >= 0) d_load<C>(a, d_ref, drow0, cd, sdr);
+    }
     // ------------------------------------------ fix-up: unpredicted ----
+    // Spread over the whole grid: task t = wave * (grid) + workgroup of the
+    // gate/up waves computes 4 rows of fix-up slot t / FT, so one miss costs
+    // each workgroup at most one wave's pass over 4 rows.
     {
-      const int mi = upos;       // this workgroup's fix-up slot and rows
-      if (mi < n_miss) {
-        const int32_t ref = miss_ref[mi];
-        u_load<C>(a, ref, urow0, cg, cu, sr);
-#pragma unroll
-        for (int it = 0; it < C::SIT; ++it) {
-          const int i = it * NT + tid;
-          if (i < 4 * SB_U4) (&sbu_l[0][0])[i] = sr[it];
-        }
-        __syncthreads();
-        if (wave < C::WAVES_U)
-          u_rows<C>(a, ref, urow0, cg, cu, act_l, asum_l, sbu_l, h_fix + (size_t)mi * F);
-      }
-      wg_arrive(counter(a, l, CNT_F0 + mi));
+      constexpr int FT = F / 4;   // tasks per expert
+      constexpr int NWG = C::ITEMS_D;
+      static_assert(K * FT <= C::WAVES_U * NWG, "every fix-up task has a wave");
+      const int t = wave * NWG + wg;
+      if (wave < C::WAVES_U && t < n_miss * FT)
+        fix_task<C>(a, miss_ref[t / FT], t % FT, act_l, asum_l, &sbu_l[0][0] + wave * 64,
+                    a.hfix + (size_t)(t / FT) * (F / 2), layer_flag(a, l));
       if (wave == 0) trace_mark(a, l, TR_FIXED);
     }
     // ------------------------------------------------------------ D_l ----
     if (wave < K) {
-      const int r = d_rank[wave], fx = d_fix[wave];
-      const int32_t dref = sel_ref[r];
+      const int r = d_r, fx = d_fx;
+      const int32_t dref = d_ref;
       const char *dw = resolve(a.pa, comp_index(PROJ_DOWN, PART_W, NP), dref);
-      if (fx >= 0) d_load<C>(a, dref, drow0, cd, sdr);   // not staged
-      wave_wait(counter(a, l, fx < 0 ? CNT_U0 + wave : CNT_F0 + fx), ep * NPOS);
+      if (fx < 0) wave_wait(counter(a, l, CNT_U0 + wave), ep * NPOS);
       if (wave == 0) trace_mark(a, l, TR_D_WAITED);
       uint4 *hact = hact_l[wave];
       float *hsum = hsum_l[wave];
@@ -651,12 +801,16 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
           const int i = it * 64 + lane;
           if (i < 2 * SBD_U4) sbd[i] = sdr[it];
         }
-        const uint16_t *hrow = (fx < 0 ? h_pred + (size_t)wave * F : h_fix + (size_t)fx * F);
         // the expert's F activations: 8 bf16 per 16-byte piece, <= 2 per lane
         static_assert(HU4 <= 128, "two pieces per lane");
         const int i0 = lane, i1 = lane + 64;
         uint4 p0, p1;
-        ld_dev_b128x2(hrow + 8 * min(i0, HU4 - 1), hrow + 8 * min(i1, HU4 - 1), p0, p1);
+        if (fx < 0) {
+          const uint16_t *hrow = h_pred + (size_t)wave * F;
+          ld_dev_b128x2(hrow + 8 * min(i0, HU4 - 1), hrow + 8 * min(i1, HU4 - 1), p0, p1);
+        } else {
+          fix_acts<HU4>(a.hfix + (size_t)fx * (F / 2), layer_flag(a, l), p0, p1);
+        }
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
           const int i = it ? i1 : i0;
