@@ -339,9 +339,9 @@ size_t moe_stack_workspace(const moe_geom *g, int32_t n_layers, int32_t E, int32
   if (!g || n_layers <= 0 || E <= 0 || k <= 0) return 0;
   const size_t counters = (size_t)n_layers * moe::kCountersPerLayer * moe::kCounterWords * 4;
   const size_t logits = ((size_t)2 * E * 8 + 255) & ~(size_t)255;   // flagged entries
-  const size_t h = ((size_t)k * g->d_ff * 2 + 255) & ~(size_t)255;      // bf16, predicted
-  const size_t hfix = ((size_t)k * (g->d_ff / 2) * 8 + 255) & ~(size_t)255;   // flagged fix-up
-  return counters + logits + h + hfix;
+  // flagged activations (2 bf16 + flag per 8 bytes): predicted, fix-up
+  const size_t h = ((size_t)k * (g->d_ff / 2) * 8 + 255) & ~(size_t)255;
+  return counters + logits + 2 * h;
 }
 
 int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_layers,
@@ -397,8 +397,8 @@ int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_lay
   ws += (size_t)n_layers * moe::kCountersPerLayer * moe::kCounterWords * 4;
   a.lgt = reinterpret_cast<uint64_t *>(ws);
   ws += ((size_t)2 * E * 8 + 255) & ~(size_t)255;
-  a.h = reinterpret_cast<uint16_t *>(ws);
-  ws += ((size_t)k * g->d_ff * 2 + 255) & ~(size_t)255;
+  a.hpred = reinterpret_cast<uint64_t *>(ws);
+  ws += ((size_t)k * (g->d_ff / 2) * 8 + 255) & ~(size_t)255;
   a.hfix = reinterpret_cast<uint64_t *>(ws);
   a.L = n_layers;
   a.E = E;

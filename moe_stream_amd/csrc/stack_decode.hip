@@ -57,8 +57,8 @@ struct StackArgs {
   int32_t *pred;          // [L][KP]
   int32_t *miss;          // [L]
   uint64_t *lgt;          // ws [2][E] router / lookahead logits, flagged (put_logit)
-  uint16_t *h;            // ws [K][F] bf16 activations of the predicted experts
-  uint64_t *hfix;         // ws [K][F/2] fix-up activations: 2 bf16 + 32-bit flag each
+  uint64_t *hpred;        // ws [K][F/2] activations of the predicted experts and
+  uint64_t *hfix;         // ws [K][F/2] of the fix-up slots: 2 bf16 + layer flag each
   uint32_t *cnt;          // ws [L][3][kSub] counters, 128 B apart
   int L, E, kp, mode, renorm, act;
   float alpha, limit;
@@ -94,14 +94,13 @@ __device__ __forceinline__ void trace_mark_after(const StackArgs &a, int l, int 
 constexpr int kSub = 8;
 constexpr int kCounterWords = kSub * 32;
 
-// Counters of one layer: router rows, lookahead rows, the layer output, one
-// per predicted position for its activations.  (Fix-up activations carry
-// their own flags instead.)
-enum { CNT_D = 0, CNT_U0 = 1 };
-constexpr int kCountersPerLayer = CNT_U0 + 8;
+// Counters of one layer: the layer output (the layer boundary).  Router
+// logits and expert activations carry their own flags instead.
+enum { CNT_D = 0 };
+constexpr int kCountersPerLayer = 1;
 
 // The flag a data entry exchanged between workgroups carries (router logits,
-// fix-up activations): unique per (token, layer), so an entry left by an
+// expert activations): unique per (token, layer), so an entry left by an
 // earlier token or layer never passes for a current one.
 __device__ __forceinline__ uint32_t layer_flag(const StackArgs &a, int l) {
   return a.epoch * (uint32_t)a.L + (uint32_t)l;
@@ -118,32 +117,6 @@ __device__ __forceinline__ void put_logit(uint64_t *slot, float v, uint32_t fl) 
 
 __device__ __forceinline__ uint32_t *counter(const StackArgs &a, int l, int which) {
   return a.cnt + ((size_t)l * kCountersPerLayer + which) * kCounterWords;
-}
-
-// Two 16-byte device-scope (sc1) loads, waited for together.
-__device__ __forceinline__ void ld_dev_b128x2(const void *p0, const void *p1, uint4 &v0,
-                                              uint4 &v1) {
-  asm volatile(
-      "global_load_dwordx4 %0, %2, off sc1\n"
-      "global_load_dwordx4 %1, %3, off sc1\n"
-      "s_waitcnt vmcnt(0)"
-      : "=&v"(v0), "=&v"(v1)
-      : "v"(p0), "v"(p1)
-      : "memory");
-}
-
-// 16 bytes at device scope (4 x sc1 dword loads issued back to back).
-__device__ __forceinline__ uint4 ld_dev16(const float *p) {
-  uint4 r;
-  r.x = __hip_atomic_load(reinterpret_cast<const uint32_t *>(p) + 0, __ATOMIC_RELAXED,
-                          __HIP_MEMORY_SCOPE_AGENT);
-  r.y = __hip_atomic_load(reinterpret_cast<const uint32_t *>(p) + 1, __ATOMIC_RELAXED,
-                          __HIP_MEMORY_SCOPE_AGENT);
-  r.z = __hip_atomic_load(reinterpret_cast<const uint32_t *>(p) + 2, __ATOMIC_RELAXED,
-                          __HIP_MEMORY_SCOPE_AGENT);
-  r.w = __hip_atomic_load(reinterpret_cast<const uint32_t *>(p) + 3, __ATOMIC_RELAXED,
-                          __HIP_MEMORY_SCOPE_AGENT);
-  return r;
 }
 
 // One whole wave: poll until the counter's sum >= target (no barrier).
@@ -249,6 +222,21 @@ struct StackCfg {
   static_assert((ROWS_U * NG * 2) % 16 == 0 && (ROWS_D * NGF * 2) % 16 == 0, "scale blocks");
 };
 
+// One whole wave, one row per 16 lanes (the row's activation in `hb` on
+// each of its lanes): the 4 rows' bf16 activations as two flagged 8-byte
+// entries (2 bf16 + layer flag) at hf[0], hf[1].
+__device__ __forceinline__ void put_acts(uint64_t *hf, uint32_t hb, uint32_t fl) {
+  const uint32_t h0 = __builtin_amdgcn_readlane(hb, 0), h1 = __builtin_amdgcn_readlane(hb, 16);
+  const uint32_t h2 = __builtin_amdgcn_readlane(hb, 32), h3 = __builtin_amdgcn_readlane(hb, 48);
+  if ((threadIdx.x & 63) == 0) {
+    const uint64_t f = (uint64_t)fl << 32;
+    __hip_atomic_store(hf, (uint64_t)(h0 | (h1 << 16)) | f, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(hf + 1, (uint64_t)(h2 | (h3 << 16)) | f, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 // Gate/up rows of one expert for this workgroup's 24-row block, waves
 // 0..WAVES_U-1: codes in cg/cu, scales staged in sbu_l, x staged in act_l
 // and asum_l.  Writes the bf16-rounded activations to hdst[row] (device
@@ -257,7 +245,8 @@ template <class C>
 __device__ __forceinline__ void u_rows(const StackArgs &a, int32_t ref, int row0,
                                        const uint4 (&cg)[C::CPLU], const uint4 (&cu)[C::CPLU],
                                        const uint4 *act_l, const float *asum_l,
-                                       const uint4 (*sbu_l)[C::SB_U4], uint16_t *hdst) {
+                                       const uint4 (*sbu_l)[C::SB_U4], uint64_t *hf,
+                                       uint32_t fl) {
   constexpr int U = C::U, NG = C::NG, SGU = C::SGU, CPLU = C::CPLU, RPSU = C::RPSU;
   constexpr int SB_U4 = C::SB_U4, NP = C::NP;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -295,15 +284,9 @@ __device__ __forceinline__ void u_rows(const StackArgs &a, int32_t ref, int row0
   } else if (lane == 0) {
     flag_error();
   }
-  // the wave's RPSU = 4 consecutive rows as one 8-byte device-scope store
+  // the wave's RPSU = 4 consecutive rows as two flagged entries (put_acts)
   static_assert(RPSU == 4, "four rows per wave");
-  const uint32_t h0 = __builtin_amdgcn_readlane(hb, 0), h1 = __builtin_amdgcn_readlane(hb, 16);
-  const uint32_t h2 = __builtin_amdgcn_readlane(hb, 32), h3 = __builtin_amdgcn_readlane(hb, 48);
-  if (lane == 0) {
-    const uint64_t v = (uint64_t)(h0 | (h1 << 16)) | ((uint64_t)(h2 | (h3 << 16)) << 32);
-    __hip_atomic_store(reinterpret_cast<uint64_t *>(hdst + row0 + wave * RPSU), v,
-                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  put_acts(hf + (row0 + wave * RPSU) / 2, hb, fl);
 }
 
 // One fix-up task, one whole wave: gate/up + activation of rows
@@ -373,22 +356,15 @@ __device__ __forceinline__ void fix_task(const StackArgs &a, int32_t ref, int b,
   uint32_t hb = 0;
   if (ok) hb = f32_to_bf16(apply_act(a.act, pg, pu, a.alpha, a.limit));
   else if (lane == 0) flag_error();
-  const uint32_t h0 = __builtin_amdgcn_readlane(hb, 0), h1 = __builtin_amdgcn_readlane(hb, 16);
-  const uint32_t h2 = __builtin_amdgcn_readlane(hb, 32), h3 = __builtin_amdgcn_readlane(hb, 48);
-  if (lane == 0) {
-    const uint64_t f = (uint64_t)fl << 32;
-    __hip_atomic_store(hf + 2 * b, (uint64_t)(h0 | (h1 << 16)) | f, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(hf + 2 * b + 1, (uint64_t)(h2 | (h3 << 16)) | f, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-  }
+  put_acts(hf + 2 * b, hb, fl);
 }
 
-// One whole wave: the F activations of fix-up slot `hf` as two 16-byte pieces
+// One whole wave: the F activations of one expert (`hf`, its F/2 flagged
+// entries) as two 16-byte pieces
 // per lane (pieces lane and lane + 64, 8 bf16 each), polled until every entry
 // carries the flag `fl`.  Bounded like wave_wait.
 template <int HU4>
-__device__ __forceinline__ void fix_acts(const uint64_t *hf, uint32_t fl, uint4 &p0, uint4 &p1) {
+__device__ __forceinline__ void get_acts(const uint64_t *hf, uint32_t fl, uint4 &p0, uint4 &p1) {
   const int lane = threadIdx.x & 63;
   const uint64_t *e0 = hf + 4 * min(lane, HU4 - 1), *e1 = hf + 4 * min(lane + 64, HU4 - 1);
   uint32_t spins = 0;
@@ -512,7 +488,6 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
   __shared__ int d_fix[K];           // D wave w: fix-up slot, or -1 (predicted at w)
   __shared__ int32_t miss_ref[K];    // fix-up slot -> slot ref
   __shared__ int n_miss;
-  __shared__ int u_done[2];          // gate/up waves finished (slot l & 1)
   __shared__ int staged[2];          // gate/up waves done staging x (slot l & 1)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -521,10 +496,8 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
   const int upos = wg / NPOS, urow0 = (wg % NPOS) * ROWS_U;   // gate/up block
   const int drow0 = wg * ROWS_D;                               // down block
   const int dj = lane % SGD, dsub = lane / SGD;
-  uint16_t *h_pred = a.h;
   if (tid < 2) {
     pred_cnt[tid] = 0;               // layer 0 has no prediction
-    u_done[tid] = 0;
     staged[tid] = 0;
   }
 
@@ -596,12 +569,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       // gate/up of the predicted expert at this workgroup's position
       if (wave < C::WAVES_U && upos < pcnt)
         u_rows<C>(a, pred_ref[l & 1][upos], urow0, cg, cu, act_l, asum_l, sbu_l,
-                  h_pred + (size_t)upos * F);
-      // the position's counter advances by NPOS every layer, work or not
-      __builtin_amdgcn_s_waitcnt(0);
-      if (lane == 0 && atomicAdd(&u_done[l & 1], 1) == W_ROUTER - 1)
-        __hip_atomic_fetch_add(counter(a, l, CNT_U0 + upos) + (wg % kSub) * 32, 1u,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                  a.hpred + (size_t)upos * (F / 2), layer_flag(a, l));
       if (wave == 0) trace_mark(a, l, TR_U_ARRIVED);
     } else if (wave == W_ROUTER) {
       // one router row (the lane partition and summation order of
@@ -752,7 +720,6 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
     __syncthreads();
     if (wave == 0) trace_mark(a, l, TR_SELECTED);
     if (tid == 0) {   // next layer's slots; nobody touches them before its start
-      u_done[(l + 1) & 1] = 0;
       staged[(l + 1) & 1] = 0;
     }
     if (wg == 0 && tid < K) {
@@ -790,8 +757,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       const int r = d_r, fx = d_fx;
       const int32_t dref = d_ref;
       const char *dw = resolve(a.pa, comp_index(PROJ_DOWN, PART_W, NP), dref);
-      if (fx < 0) wave_wait(counter(a, l, CNT_U0 + wave), ep * NPOS);
-      if (wave == 0) trace_mark(a, l, TR_D_WAITED);
+
       uint4 *hact = hact_l[wave];
       float *hsum = hsum_l[wave];
       if (dw != nullptr) {
@@ -805,12 +771,9 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
         static_assert(HU4 <= 128, "two pieces per lane");
         const int i0 = lane, i1 = lane + 64;
         uint4 p0, p1;
-        if (fx < 0) {
-          const uint16_t *hrow = h_pred + (size_t)wave * F;
-          ld_dev_b128x2(hrow + 8 * min(i0, HU4 - 1), hrow + 8 * min(i1, HU4 - 1), p0, p1);
-        } else {
-          fix_acts<HU4>(a.hfix + (size_t)fx * (F / 2), layer_flag(a, l), p0, p1);
-        }
+        get_acts<HU4>(fx < 0 ? a.hpred + (size_t)wave * (F / 2) : a.hfix + (size_t)fx * (F / 2),
+                      layer_flag(a, l), p0, p1);
+        if (wave == 0) trace_mark(a, l, TR_D_WAITED);
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
           const int i = it ? i1 : i0;
