@@ -339,9 +339,10 @@ size_t moe_stack_workspace(const moe_geom *g, int32_t n_layers, int32_t E, int32
   if (!g || n_layers <= 0 || E <= 0 || k <= 0) return 0;
   const size_t counters = (size_t)n_layers * moe::kCountersPerLayer * moe::kCounterWords * 4;
   const size_t logits = ((size_t)2 * E * 8 + 255) & ~(size_t)255;   // flagged entries
-  // flagged activations (2 bf16 + flag per 8 bytes): predicted, fix-up
-  const size_t h = ((size_t)k * (g->d_ff / 2) * 8 + 255) & ~(size_t)255;
-  return counters + logits + 2 * h;
+  // flagged activations (2 bf16 + flag per 8 bytes): predicted (+ spares), fix-up
+  const size_t hp = ((size_t)(k + moe::kSpare) * (g->d_ff / 2) * 8 + 255) & ~(size_t)255;
+  const size_t hf = ((size_t)k * (g->d_ff / 2) * 8 + 255) & ~(size_t)255;
+  return counters + logits + hp + hf;
 }
 
 int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_layers,
@@ -398,7 +399,7 @@ int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_lay
   a.lgt = reinterpret_cast<uint64_t *>(ws);
   ws += ((size_t)2 * E * 8 + 255) & ~(size_t)255;
   a.hpred = reinterpret_cast<uint64_t *>(ws);
-  ws += ((size_t)k * (g->d_ff / 2) * 8 + 255) & ~(size_t)255;
+  ws += ((size_t)(k + moe::kSpare) * (g->d_ff / 2) * 8 + 255) & ~(size_t)255;
   a.hfix = reinterpret_cast<uint64_t *>(ws);
   a.L = n_layers;
   a.E = E;

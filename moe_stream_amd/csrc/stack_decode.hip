@@ -57,7 +57,7 @@ struct StackArgs {
   int32_t *pred;          // [L][KP]
   int32_t *miss;          // [L]
   uint64_t *lgt;          // ws [2][E] router / lookahead logits, flagged (put_logit)
-  uint64_t *hpred;        // ws [K][F/2] activations of the predicted experts and
+  uint64_t *hpred;        // ws [K + kSpare][F/2] activations of the predicted experts and
   uint64_t *hfix;         // ws [K][F/2] of the fix-up slots: 2 bf16 + layer flag each
   uint32_t *cnt;          // ws [L][3][kSub] counters, 128 B apart
   int L, E, kp, mode, renorm, act;
@@ -93,6 +93,11 @@ __device__ __forceinline__ void trace_mark_after(const StackArgs &a, int l, int 
 // spread by workgroup id), so 256 arrivals do not queue on one address.
 constexpr int kSub = 8;
 constexpr int kCounterWords = kSub * 32;
+
+// Predicted experts beyond the K staged ones whose gate/up the workgroups
+// compute speculatively from the pool each layer (lookahead ranks K ..
+// K + kSpare - 1): a routed expert among them needs no fix-up pass.
+constexpr int kSpare = 2;
 
 // Counters of one layer: the layer output (the layer boundary).  Router
 // logits and expert activations carry their own flags instead.
@@ -470,6 +475,9 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
   constexpr int W_ROUTER = 6, W_RANK = 7;    // the router wave and the ranking wave
   static_assert(C::WAVES_U <= W_ROUTER && NT / 64 == 8, "wave roles");
   static_assert(C::ITEMS_U == K * NPOS, "one gate/up block per (position, row block)");
+  constexpr int FT = F / 4;          // 4-row tasks per expert (fix-up, spares)
+  constexpr int NWG = C::ITEMS_D;    // the grid
+  static_assert(K * FT <= C::WAVES_U * NWG && kSpare <= K, "every task has a wave");
 
   __shared__ uint4 act_l[4 * U];
   __shared__ float asum_l[U];
@@ -481,12 +489,14 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
   __shared__ int sel_id[K];
   __shared__ float sel_sc[K];
   __shared__ int32_t sel_ref[K];
-  __shared__ int pred_buf[2][K];     // lookahead's K best, rank order (slot l & 1)
-  __shared__ int32_t pred_ref[2][K]; // their slot refs (looked up by the ranking wave)
-  __shared__ int pred_cnt[2];
+  __shared__ int pred_buf[2][K + kSpare];      // lookahead's best, rank order (slot l & 1)
+  __shared__ int32_t pred_ref[2][K + kSpare];  // their slot refs (looked up by the ranking wave)
+  __shared__ int pred_cnt[2];                  // staged positions (<= K)
+  __shared__ int spare_cnt[2];                 // spare positions (<= kSpare)
   __shared__ int d_rank[K];          // D wave w: routing rank of its expert
   __shared__ int d_fix[K];           // D wave w: fix-up slot, or -1 (predicted at w)
   __shared__ int32_t miss_ref[K];    // fix-up slot -> slot ref
+  __shared__ int miss_src[K];        // i-th unstaged routed expert: fix-up slot, or -1 - spare
   __shared__ int n_miss;
   __shared__ int staged[2];          // gate/up waves done staging x (slot l & 1)
 
@@ -498,6 +508,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
   const int dj = lane % SGD, dsub = lane / SGD;
   if (tid < 2) {
     pred_cnt[tid] = 0;               // layer 0 has no prediction
+    spare_cnt[tid] = 0;
     staged[tid] = 0;
   }
 
@@ -570,6 +581,14 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       if (wave < C::WAVES_U && upos < pcnt)
         u_rows<C>(a, pred_ref[l & 1][upos], urow0, cg, cu, act_l, asum_l, sbu_l,
                   a.hpred + (size_t)upos * (F / 2), layer_flag(a, l));
+      // the spare positions, spread over the grid (task t: 4 rows of spare
+      // t / FT), straight from the pool while the routing runs
+      {
+        const int t = wave * NWG + wg;
+        if (wave < C::WAVES_U && t < spare_cnt[l & 1] * FT)
+          fix_task<C>(a, pred_ref[l & 1][K + t / FT], t % FT, act_l, asum_l, hact_l[wave],
+                      a.hpred + (size_t)(K + t / FT) * (F / 2), layer_flag(a, l));
+      }
       if (wave == 0) trace_mark(a, l, TR_U_ARRIVED);
     } else if (wave == W_ROUTER) {
       // one router row (the lane partition and summation order of
@@ -609,23 +628,29 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
         const float z1 = e1 < a.E ? round_bf16(l1 + b1) : -INFINITY;
         bool s0, s1;
         int r0, r1;
-        select_topk(e0 < a.E ? order_key(z0) : -1, e1 < a.E ? order_key(z1) : -1, a.kp, lane,
+        // the caller's k_pred, and at least the K staged + kSpare spare
+        // positions for this kernel's own speculation
+        const int ksel = min(max(a.kp, K + kSpare), a.E);
+        select_topk(e0 < a.E ? order_key(z0) : -1, e1 < a.E ? order_key(z1) : -1, ksel, lane,
                     s0, s1, r0, r1);
         if (wg == 0) {
-          if (s0) a.pred[(size_t)l * a.kp + r0] = e0;
-          if (s1) a.pred[(size_t)l * a.kp + r1] = e1;
+          if (s0 && r0 < a.kp) a.pred[(size_t)l * a.kp + r0] = e0;
+          if (s1 && r1 < a.kp) a.pred[(size_t)l * a.kp + r1] = e1;
         }
         int *pn = pred_buf[(l + 1) & 1];
         int32_t *pr = pred_ref[(l + 1) & 1];
-        if (s0 && r0 < K) {
+        if (s0 && r0 < K + kSpare) {
           pn[r0] = e0;
           pr[r0] = t0;
         }
-        if (s1 && r1 < K) {
+        if (s1 && r1 < K + kSpare) {
           pn[r1] = e1;
           pr[r1] = t1;
         }
-        if (lane == 0) pred_cnt[(l + 1) & 1] = min(a.kp, K);
+        if (lane == 0) {
+          pred_cnt[(l + 1) & 1] = min(a.kp, K);
+          spare_cnt[(l + 1) & 1] = max(0, ksel - K);
+        }
       }
     } else {
       // ---- routing: every workgroup ranks this layer's logits ----------
@@ -690,19 +715,26 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
       const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
       bool miss = false, routed = false;
-      int rank_w = -1;
+      int rank_w = -1, sp = -1;
       int32_t ref_r = 0;
+      const int nsp = spare_cnt[l & 1];
       if (lane < K) {
         const int er = sel_id[lane];   // routed expert of rank `lane`
         ref_r = sel_ref[lane];
         miss = true;
         for (int p = 0; p < pcnt; ++p) miss = miss && (P[p] != er);
+        for (int q = 0; q < nsp; ++q)
+          if (P[K + q] == er) sp = q;    // computed at a spare position
         const int pw = lane < pcnt ? P[lane] : -1;   // predicted expert at position `lane`
         for (int r = 0; r < K; ++r)
           if (pw >= 0 && sel_id[r] == pw) { routed = true; rank_w = r; }
       }
+      // unstaged routed experts (rank order): a spare's activations are
+      // ready; the others (true misses) get fix-up slots
       const uint64_t mm = __ballot(miss), fm = __ballot(lane < K && !routed);
-      if (miss) miss_ref[__popcll(mm & below)] = ref_r;
+      const uint64_t tm = __ballot(miss && sp < 0);
+      if (miss && sp < 0) miss_ref[__popcll(tm & below)] = ref_r;
+      if (miss) miss_src[__popcll(mm & below)] = sp >= 0 ? -1 - sp : __popcll(tm & below);
       if (lane < K) {
         if (routed) {
           d_rank[lane] = rank_w;
@@ -715,7 +747,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
           d_fix[lane] = fi;
         }
       }
-      if (lane == 0) n_miss = __popcll(mm);
+      if (lane == 0) n_miss = __popcll(tm);
     }
     __syncthreads();
     if (wave == 0) trace_mark(a, l, TR_SELECTED);
@@ -743,12 +775,9 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
     // gate/up waves computes 4 rows of fix-up slot t / FT, so one miss costs
     // each workgroup at most one wave's pass over 4 rows.
     {
-      constexpr int FT = F / 4;   // tasks per expert
-      constexpr int NWG = C::ITEMS_D;
-      static_assert(K * FT <= C::WAVES_U * NWG, "every fix-up task has a wave");
       const int t = wave * NWG + wg;
       if (wave < C::WAVES_U && t < n_miss * FT)
-        fix_task<C>(a, miss_ref[t / FT], t % FT, act_l, asum_l, &sbu_l[0][0] + wave * 64,
+        fix_task<C>(a, miss_ref[t / FT], t % FT, act_l, asum_l, hact_l[wave],
                     a.hfix + (size_t)(t / FT) * (F / 2), layer_flag(a, l));
       if (wave == 0) trace_mark(a, l, TR_FIXED);
     }
@@ -771,8 +800,11 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
         static_assert(HU4 <= 128, "two pieces per lane");
         const int i0 = lane, i1 = lane + 64;
         uint4 p0, p1;
-        get_acts<HU4>(fx < 0 ? a.hpred + (size_t)wave * (F / 2) : a.hfix + (size_t)fx * (F / 2),
-                      layer_flag(a, l), p0, p1);
+        const int src = fx < 0 ? 0 : miss_src[fx];
+        const uint64_t *hf = fx < 0    ? a.hpred + (size_t)wave * (F / 2)
+                             : src >= 0 ? a.hfix + (size_t)src * (F / 2)
+                                        : a.hpred + (size_t)(K - 1 - src) * (F / 2);
+        get_acts<HU4>(hf, layer_flag(a, l), p0, p1);
         if (wave == 0) trace_mark(a, l, TR_D_WAITED);
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
