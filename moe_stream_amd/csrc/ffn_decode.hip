@@ -401,11 +401,17 @@ static size_t down_lds_bytes(int k) {
 
 // d_model, d_ff, proj bias | gate/up: SG, waves, row steps | down: SG, steps
 static const FfnLaunch kFfnTable[] = {
-    // Qwen3-30B-A3B: 24 rows per workgroup -> 8 experts x 32 = 256 WGs
+    // Launch shapes from a sweep on MI355X (kernel time, rotating slots).
+    // Qwen3-30B-A3B: 24 rows per workgroup -> 8 experts x 32 = 256 WGs.  Its
+    // lane split (16 lanes per row, 4 chunks each) is the persistent
+    // kernel's, so both paths sum every row in the same order and produce
+    // identical bits (8 rows of 32 lanes measured 6.1 vs 7.0 us but would
+    // break that).  gpt-oss: gate/up 8 rows 9.9 vs 10.3 us, down 8 rows of
+    // 16 lanes 8.7 vs 9.1 us.
     MOE_FFN_GEOM(2048, 768, false, 16, 6, 1, 8, 1),
     MOE_FFN_GEOM(2048, 768, true, 16, 6, 1, 8, 1),
-    MOE_FFN_GEOM(2880, 2880, true, 32, 4, 2, 32, 4),  // gpt-oss-120b
-    MOE_FFN_GEOM(2880, 2880, false, 32, 4, 2, 32, 4),
+    MOE_FFN_GEOM(2880, 2880, true, 32, 4, 1, 16, 2),  // gpt-oss-120b
+    MOE_FFN_GEOM(2880, 2880, false, 32, 4, 1, 16, 2),
     MOE_FFN_GEOM(256, 128, false, 8, 2, 1, 4, 1),     // small test geometry
     MOE_FFN_GEOM(256, 128, true, 8, 2, 1, 4, 1),
 };
