@@ -45,6 +45,9 @@ def parse():
                     help="persistent: one launch per token; graph/eager: 3 launches per layer")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--engine", default="native", choices=["native", "python"],
+                    help="qwen3-stream: the per-layer engine loop in the library "
+                         "(moe_engine_layer) or in Python (MoEBlock.streaming_call)")
     ap.add_argument("--profile-tokens", type=int, default=8,
                     help="tokens of the kernel-timing pass after the timed steps")
     return ap.parse_args()
@@ -229,8 +232,12 @@ def stream(args):
     geom, L, slots = G.QWEN3_30B_A3B, 48, 2048
     n_tok = args.tokens if args.tokens != 64 else 256
     t_build = time.perf_counter()
-    st = StreamingStack(geom, L, slots, dev, zipf_s=1.1)
+    native = args.engine == "native"
+    st = StreamingStack(geom, L, slots, dev, zipf_s=1.1, native=native)
     t_build = time.perf_counter() - t_build
+
+    def bytes_read():
+        return st.engine_counters()["bytes_read"] if native else st.pool.bytes_read
     xs = synth.hidden_states(n_tok + args.warmup, L, geom.d_model, dev, synth.SEED_BASE + 400)
     # pinned host -> HBM copy rate on this box (1 GiB, one hipMemcpyAsync)
     h = torch.empty(1 << 30, dtype=torch.uint8).pin_memory()
@@ -248,7 +255,7 @@ def stream(args):
         st.token(xs[t])
     torch.cuda.synchronize()
     s0 = st.pool.stats()
-    b0 = st.pool.bytes_read
+    b0 = bytes_read()
     y = torch.empty((L, geom.d_model), dtype=torch.bfloat16, device=dev)
     t0 = time.perf_counter()
     for t in range(args.warmup, args.warmup + n_tok):
@@ -259,7 +266,7 @@ def stream(args):
     ops.check_device_error()
     s1 = st.pool.stats()
     d = {k: s1[k] - s0[k] for k in ("total", "prefetch", "cache", "miss", "bail", "issued")}
-    copied = st.pool.bytes_read - b0
+    copied = bytes_read() - b0
     out = {"metric": "MoE streaming decode tok/s (bs=1, 48 layers, 2048-slot pool, "
                      "pinned host store)",
            "value": round(n_tok / wall, 2), "unit": "tok/s", "n_gpus": 1, "steps": 1,
@@ -270,6 +277,8 @@ def stream(args):
                       "pool_slots": slots, "store_records": L * geom.n_experts,
                       "record_bytes": geom.record_bytes, "tokens": n_tok,
                       "evict": st.pool.evict, "prefetch": "lookahead depth 1, widen 1",
+                      "engine": ("moe_engine_layer (library)" if native
+                                 else "MoEBlock.streaming_call (Python)"),
                       "router_bias": "zipf(1.1) log-popularity",
                       "parallelism": "none (1 GPU)"},
            "hit_rate": round((d["prefetch"] + d["cache"]) / max(1, d["total"]), 4),

@@ -224,8 +224,10 @@ int moe_slot_lookup(const int32_t *table, int32_t E, const int32_t *ids,
 /* Slot fills: copy n whole expert records into pool slots.
  * src_records: record indices into `src_store` (host pinned or device
  * memory laid out like pool->store; NULL means pool->store), dst_slots: pool
- * slots.  Host index arrays.  Enqueued on `stream` (hipMemcpyAsync per
- * component).  Replaces ExpertPool._read (engine_v3.py:255-290). */
+ * slots.  Host index arrays.  Enqueued on `stream`: a source the GPU can
+ * read (HBM or pinned host memory) is copied by kernels, up to 160 records
+ * per launch; pageable memory by hipMemcpyAsync per component.  Replaces
+ * ExpertPool._read (engine_v3.py:255-290). */
 int moe_fill_slots(const moe_pool_view *pool, const void *src_store,
                    int64_t src_record_bytes, const int64_t *src_records,
                    const int32_t *dst_slots, int32_t n, void *stream);
@@ -285,6 +287,38 @@ int moe_policy_table(const moe_policy *p, int32_t *table);
 /* out[8] = total, prefetch hits, cache hits, misses, prefetch bails,
  * prefetches issued, allocation clock, use clock */
 int moe_policy_stats(const moe_policy *p, int64_t *out);
+
+/*
+ * Native per-layer engine loop of the streaming pool, bs=1 decode: the steps
+ * of streaming_call (engine_v3.py:493-609) -- route + lookahead, one host
+ * synchronisation, prefetch of the predicted next-layer experts
+ * (ExpertPool.prefetch, engine_v3.py:383-396) as fills on side_stream,
+ * acquire (ExpertPool.acquire, :398-454) with misses filled on
+ * compute_stream and in-flight prefetches turned into stream waits, then the
+ * expert block -- without returning to the caller in between.  `policy` is
+ * the pool's slot policy (moe_policy_create), shared with the caller;
+ * `store` holds n_records records of record_bytes (pinned host memory for
+ * DMA fills, or device memory).  moe_engine_layer is synchronous up to the
+ * routing (it waits for the layer's route kernel) and leaves the expert
+ * block enqueued on compute_stream.  The engine owns the events of its
+ * pending prefetches; a pool driven by an engine is not filled by anyone
+ * else meanwhile.
+ */
+typedef struct moe_engine moe_engine;
+int moe_engine_create(const moe_pool_view *pool, const moe_geom *g, int32_t n_layers,
+                      int32_t E, int32_t k, int32_t k_pred, moe_policy *policy,
+                      const void *store, int64_t record_bytes, int64_t n_records,
+                      void *compute_stream, void *side_stream, moe_engine **out);
+int moe_engine_destroy(moe_engine *e);
+/* One layer: x [1, d_model] bf16 -> y [1, d_model] bf16.  W_next/bias_next:
+ * the next layer's router for the lookahead (NULL at the last layer). */
+int moe_engine_layer(moe_engine *e, int32_t layer, const uint16_t *x, const uint16_t *W,
+                     const uint16_t *bias, int32_t mode, int32_t renorm,
+                     const uint16_t *W_next, const uint16_t *bias_next, uint16_t *y);
+/* out[5] = bytes read into the pool, bytes read on the critical path
+ * (misses), routed experts that were predicted, routed experts counted for
+ * recall, prefetches still pending */
+int moe_engine_counters(const moe_engine *e, int64_t *out);
 
 #ifdef __cplusplus
 }

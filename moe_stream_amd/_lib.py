@@ -42,6 +42,7 @@ EXPORTS = (
     "moe_policy_create", "moe_policy_destroy", "moe_policy_prefetch",
     "moe_policy_acquire", "moe_policy_complete", "moe_policy_lookup",
     "moe_policy_is_pending", "moe_policy_table", "moe_policy_stats",
+    "moe_engine_create", "moe_engine_destroy", "moe_engine_layer", "moe_engine_counters",
 )
 
 MOE_EVICT_LFU = 0
@@ -118,6 +119,11 @@ def _declare(lib):
         "moe_policy_is_pending": (C.c_int, [P, I32, I32]),
         "moe_policy_table": (C.c_int, [P, P]),
         "moe_policy_stats": (C.c_int, [P, P]),
+        "moe_engine_create": (C.c_int, [C.POINTER(PoolView), C.POINTER(Geom), I32, I32, I32,
+                                        I32, P, P, I64, I64, P, P, C.POINTER(C.c_void_p)]),
+        "moe_engine_destroy": (C.c_int, [P]),
+        "moe_engine_layer": (C.c_int, [P, I32, P, P, P, I32, I32, P, P, P]),
+        "moe_engine_counters": (C.c_int, [P, P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)

@@ -480,13 +480,19 @@ __global__ __launch_bounds__(256) void fill_slots_kernel(const FillArgs a) {
   for (; j < n16; j += 256) d[j] = s[j];
 }
 
-bool device_memory(const void *p) {
+// The address a kernel reads `p` through: device memory as is, pinned host
+// memory (hipHostMalloc) through its device mapping; nullptr for pageable
+// host memory, which only a copy engine can read.
+const char *kernel_address(const void *p) {
   hipPointerAttribute_t at;
   if (hipPointerGetAttributes(&at, p) != hipSuccess) {
     (void)hipGetLastError();
-    return false;
+    return nullptr;
   }
-  return at.type == hipMemoryTypeDevice;
+  if (at.type == hipMemoryTypeDevice) return static_cast<const char *>(p);
+  if (at.type == hipMemoryTypeHost && at.devicePointer)
+    return static_cast<const char *>(at.devicePointer);
+  return nullptr;
 }
 
 }  // namespace
@@ -512,8 +518,12 @@ int moe_fill_slots(const moe_pool_view *pool, const void *src_store,
     if (rec < 0 || (!src_store && rec >= pool->n_records))
       return fail(MOE_ERR_INVALID, "record %lld out of range", (long long)rec);
   }
-  // a device-resident source with 16-byte aligned pieces: copy kernels
-  bool kernel = device_memory(src) && aligned(src, 16) && rb % 16 == 0;
+  // Copy kernels for a source the GPU can read (HBM, or pinned host memory
+  // over the link: one launch per batch instead of a copy call per
+  // component, whose host-side cost dominated the streaming loop) with
+  // 16-byte aligned pieces; pageable memory goes through hipMemcpyAsync.
+  const char *ksrc = kernel_address(src);
+  bool kernel = ksrc != nullptr && aligned(ksrc, 16) && rb % 16 == 0;
   FillArgs fa{};
   int32_t chunks = 0;
   for (int c = 0; c < nc && kernel; ++c) {
@@ -527,7 +537,7 @@ int moe_fill_slots(const moe_pool_view *pool, const void *src_store,
   }
   if (kernel) {
     fa.chunk0[nc] = chunks;
-    fa.src = src;
+    fa.src = ksrc;
     fa.record_bytes = rb;
     fa.nc = nc;
     for (int32_t i0 = 0; i0 < n; i0 += kFillBatch) {

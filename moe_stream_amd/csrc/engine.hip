@@ -1,0 +1,283 @@
+// Native per-layer engine loop of the streaming pool for bs=1 decode: the
+// steps of streaming_call (engine_v3.py:493-609) without a Python frame in
+// between.  Per layer, in the reference's order:
+//   1. route + one lookahead (engine_v3.py:509-515) on the compute stream;
+//   2. the layer's ids and predictions to pinned host memory, ONE host
+//      synchronisation (engine_v3.py:515);
+//   3. recall bookkeeping of the previous layer's prediction (:521-523);
+//   4. prefetch of the predicted layer-(l+1) experts (:521-527, ExpertPool.
+//      prefetch :383-396): fills from the pinned host store on the side
+//      stream, one event per prefetch batch, pending until retired;
+//   5. acquire (:537-552, ExpertPool.acquire :398-454): misses filled on the
+//      compute stream, in-flight prefetches become stream waits;
+//   6. slot refs to the device (pinned host -> HBM, async) and the expert
+//      block (the decode kernels) on the compute stream.
+// The slot policy is the same native policy ExpertPool uses; the engine owns
+// the pending fills' events.
+
+#include <unordered_map>
+#include <vector>
+
+namespace {
+
+constexpr int kEngineMaxPred = 64;
+
+struct PendingFill {
+  hipEvent_t ev;
+};
+
+}  // namespace
+
+struct moe_engine {
+  moe_pool_view pool;
+  moe_geom geom;
+  moe_policy *policy = nullptr;
+  const char *store = nullptr;      // pinned host (or device) records
+  int64_t record_bytes = 0, n_records = 0;
+  int32_t L = 0, E = 0, k = 0, kp = 0;
+  hipStream_t compute = nullptr, side = nullptr;
+  // device buffers
+  int32_t *d_ids = nullptr, *d_pred = nullptr, *d_refs = nullptr;
+  float *d_scores = nullptr;
+  void *d_route_ws = nullptr, *d_ffn_ws = nullptr;
+  size_t route_ws_bytes = 0, ffn_ws_bytes = 0;
+  // pinned host staging
+  int32_t *h_ids = nullptr, *h_pred = nullptr, *h_refs = nullptr;
+  // bookkeeping
+  std::unordered_map<int64_t, hipEvent_t> pending;   // key -> its fill's event
+  std::vector<hipEvent_t> free_events;
+  std::vector<int32_t> last_pred;                    // unique prediction for layer l+1
+  int32_t last_pred_layer = -1;
+  int64_t bytes_read = 0, bytes_exposed = 0, recall_hit = 0, recall_total = 0;
+};
+
+namespace {
+
+int64_t engine_key(const moe_engine *e, int32_t layer, int32_t expert) {
+  return (int64_t)layer * e->E + expert;
+}
+
+int engine_event(moe_engine *e, hipEvent_t *ev) {
+  if (!e->free_events.empty()) {
+    *ev = e->free_events.back();
+    e->free_events.pop_back();
+    return MOE_OK;
+  }
+  MOE_HIP(hipEventCreateWithFlags(ev, hipEventDisableTiming));
+  return MOE_OK;
+}
+
+// Retire prefetch fills whose events completed (the worker epilogue,
+// engine_v3.py:292-301).  One event may cover several keys.
+int engine_poll(moe_engine *e) {
+  std::vector<hipEvent_t> done;
+  for (auto it = e->pending.begin(); it != e->pending.end();) {
+    const hipError_t q = hipEventQuery(it->second);
+    if (q == hipSuccess) {
+      moe_policy_complete(e->policy, (int32_t)(it->first / e->E), (int32_t)(it->first % e->E));
+      done.push_back(it->second);
+      it = e->pending.erase(it);
+    } else if (q == hipErrorNotReady) {
+      ++it;
+    } else {
+      return hip_fail(q, "hipEventQuery");
+    }
+  }
+  for (hipEvent_t ev : done) {
+    bool shared = false;
+    for (const auto &kv : e->pending) shared = shared || kv.second == ev;
+    bool listed = false;
+    for (hipEvent_t f : e->free_events) listed = listed || f == ev;
+    if (!shared && !listed) e->free_events.push_back(ev);
+  }
+  return MOE_OK;
+}
+
+int engine_fill(moe_engine *e, int32_t layer, const int32_t *experts, const int32_t *slots,
+                int32_t n, hipStream_t s) {
+  if (n <= 0) return MOE_OK;
+  std::vector<int64_t> recs(n);
+  for (int32_t i = 0; i < n; ++i) recs[i] = (int64_t)layer * e->E + experts[i];
+  const int rc = moe_fill_slots(&e->pool, e->store, e->record_bytes, recs.data(), slots, n, s);
+  if (rc) return rc;
+  e->bytes_read += (int64_t)n * e->record_bytes;
+  return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_engine_create(const moe_pool_view *pool, const moe_geom *g, int32_t n_layers,
+                      int32_t E, int32_t k, int32_t k_pred, moe_policy *policy,
+                      const void *store, int64_t record_bytes, int64_t n_records,
+                      void *compute_stream, void *side_stream, moe_engine **out) {
+  if (!out) return fail(MOE_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  if (!pool || !g || !policy || !store) return fail(MOE_ERR_INVALID, "NULL pool/geom/policy/store");
+  if (n_layers <= 0 || E <= 0 || E > moe::kRouteMaxE || k <= 0 || k > MOE_MAX_TOPK || k > E)
+    return fail(MOE_ERR_INVALID, "n_layers=%d E=%d k=%d", n_layers, E, k);
+  if (k_pred <= 0 || k_pred > E || k_pred > kEngineMaxPred)
+    return fail(MOE_ERR_INVALID, "k_pred=%d outside [1, min(E, %d)]", k_pred, kEngineMaxPred);
+  if (record_bytes <= 0 || n_records < (int64_t)n_layers * E)
+    return fail(MOE_ERR_INVALID, "store has %lld records of %lld bytes, need %lld",
+                (long long)n_records, (long long)record_bytes, (long long)n_layers * E);
+  moe::PoolArgs pa;
+  const int rc = make_pool_args(pool, g, &pa);
+  if (rc) return rc;
+  if (!moe::find_ffn(g->d_model, g->d_ff, g->has_proj_bias))
+    return fail(MOE_ERR_UNSUPPORTED, "no decode kernel for d_model=%d d_ff=%d", g->d_model,
+                g->d_ff);
+  moe_engine *e = new moe_engine();
+  e->pool = *pool;
+  e->geom = *g;
+  e->policy = policy;
+  e->store = static_cast<const char *>(store);
+  e->record_bytes = record_bytes;
+  e->n_records = n_records;
+  e->L = n_layers;
+  e->E = E;
+  e->k = k;
+  e->kp = k_pred;
+  e->compute = static_cast<hipStream_t>(compute_stream);
+  e->side = static_cast<hipStream_t>(side_stream);
+  e->route_ws_bytes = moe_route_workspace(1, E);
+  e->ffn_ws_bytes = moe_ffn_decode_workspace(g, 1, k);
+  hipError_t err = hipSuccess;
+  auto dmalloc = [&](void **p, size_t b) {
+    if (err == hipSuccess) err = hipMalloc(p, b);
+    if (err == hipSuccess) err = hipMemset(*p, 0, b);
+  };
+  dmalloc(reinterpret_cast<void **>(&e->d_ids), 256);
+  dmalloc(reinterpret_cast<void **>(&e->d_pred), 256);
+  dmalloc(reinterpret_cast<void **>(&e->d_refs), 256);
+  dmalloc(reinterpret_cast<void **>(&e->d_scores), 256);
+  dmalloc(&e->d_route_ws, e->route_ws_bytes);
+  dmalloc(&e->d_ffn_ws, e->ffn_ws_bytes);
+  if (err == hipSuccess) err = hipHostMalloc(reinterpret_cast<void **>(&e->h_ids), 256);
+  if (err == hipSuccess) err = hipHostMalloc(reinterpret_cast<void **>(&e->h_pred), 256);
+  if (err == hipSuccess) err = hipHostMalloc(reinterpret_cast<void **>(&e->h_refs), 256);
+  if (err != hipSuccess) {
+    moe_engine_destroy(e);
+    return hip_fail(err, "engine buffers");
+  }
+  *out = e;
+  return MOE_OK;
+}
+
+int moe_engine_destroy(moe_engine *e) {
+  if (!e) return MOE_OK;
+  if (e->compute) (void)hipStreamSynchronize(e->compute);
+  if (e->side) (void)hipStreamSynchronize(e->side);
+  std::vector<hipEvent_t> evs = e->free_events;
+  for (const auto &kv : e->pending) evs.push_back(kv.second);
+  std::sort(evs.begin(), evs.end());
+  evs.erase(std::unique(evs.begin(), evs.end()), evs.end());
+  for (hipEvent_t ev : evs) (void)hipEventDestroy(ev);
+  (void)hipFree(e->d_ids);
+  (void)hipFree(e->d_pred);
+  (void)hipFree(e->d_refs);
+  (void)hipFree(e->d_scores);
+  (void)hipFree(e->d_route_ws);
+  (void)hipFree(e->d_ffn_ws);
+  (void)hipHostFree(e->h_ids);
+  (void)hipHostFree(e->h_pred);
+  (void)hipHostFree(e->h_refs);
+  delete e;
+  return MOE_OK;
+}
+
+int moe_engine_layer(moe_engine *e, int32_t layer, const uint16_t *x, const uint16_t *W,
+                     const uint16_t *bias, int32_t mode, int32_t renorm,
+                     const uint16_t *W_next, const uint16_t *bias_next, uint16_t *y) {
+  if (!e) return fail(MOE_ERR_INVALID, "engine is NULL");
+  if (layer < 0 || layer >= e->L) return fail(MOE_ERR_INVALID, "layer %d outside [0, %d)", layer, e->L);
+  if (!x || !W || !y) return fail(MOE_ERR_INVALID, "NULL x/W/y");
+  const bool look = W_next != nullptr && layer + 1 < e->L;
+  // 1. route + lookahead
+  int rc = moe_route(x, 1, e->geom.d_model, W, bias, e->E, mode, renorm, e->k, e->d_ids,
+                     e->d_scores, look ? W_next : nullptr, look ? bias_next : nullptr, e->kp,
+                     look ? e->d_pred : nullptr, nullptr, nullptr, nullptr, e->d_route_ws,
+                     e->route_ws_bytes, e->compute);
+  if (rc) return rc;
+  // 2. one host synchronisation for routing and speculation
+  MOE_HIP(hipMemcpyAsync(e->h_ids, e->d_ids, (size_t)e->k * 4, hipMemcpyDeviceToHost, e->compute));
+  if (look)
+    MOE_HIP(hipMemcpyAsync(e->h_pred, e->d_pred, (size_t)e->kp * 4, hipMemcpyDeviceToHost,
+                           e->compute));
+  MOE_HIP(hipStreamSynchronize(e->compute));
+  // 3. recall of the prediction made for this layer
+  if (e->last_pred_layer == layer) {
+    int32_t hit = 0;
+    for (int32_t i = 0; i < e->k; ++i)
+      for (int32_t p : e->last_pred) hit += p == e->h_ids[i];
+    e->recall_hit += hit;
+    e->recall_total += e->k;
+  }
+  rc = engine_poll(e);
+  if (rc) return rc;
+  // 4. prefetch of layer + 1 (unique predicted ids, ascending, as np.unique)
+  if (look) {
+    std::vector<int32_t> up(e->h_pred, e->h_pred + e->kp);
+    std::sort(up.begin(), up.end());
+    up.erase(std::unique(up.begin(), up.end()), up.end());
+    e->last_pred = up;
+    e->last_pred_layer = layer + 1;
+    int32_t slots[kEngineMaxPred], exps[kEngineMaxPred], bailed = 0;
+    const int n = moe_policy_prefetch(e->policy, layer + 1, up.data(), (int32_t)up.size(), slots,
+                                      exps, &bailed);
+    if (n < 0) return fail(n, "policy prefetch failed");
+    if (n > 0) {
+      rc = engine_fill(e, layer + 1, exps, slots, n, e->side);
+      if (rc) return rc;
+      hipEvent_t ev;
+      rc = engine_event(e, &ev);
+      if (rc) return rc;
+      MOE_HIP(hipEventRecord(ev, e->side));
+      for (int i = 0; i < n; ++i) e->pending[engine_key(e, layer + 1, exps[i])] = ev;
+    }
+  }
+  // 5. acquire: misses on the compute stream, pending prefetches as waits
+  int32_t miss_idx[MOE_MAX_TOPK], wait_idx[MOE_MAX_TOPK], n_miss = 0, n_wait = 0;
+  rc = moe_policy_acquire(e->policy, layer, e->h_ids, e->k, e->h_refs, miss_idx, &n_miss,
+                          wait_idx, &n_wait);
+  if (rc) return fail(rc, rc == MOE_ERR_EXHAUSTED ? "pool exhausted: every slot pinned or pending"
+                                                  : "policy acquire failed");
+  if (n_miss > 0) {
+    int32_t exps[MOE_MAX_TOPK], slots[MOE_MAX_TOPK];
+    for (int32_t i = 0; i < n_miss; ++i) {
+      exps[i] = e->h_ids[miss_idx[i]];
+      slots[i] = e->h_refs[miss_idx[i]];
+    }
+    rc = engine_fill(e, layer, exps, slots, n_miss, e->compute);
+    if (rc) return rc;
+    e->bytes_exposed += (int64_t)n_miss * e->record_bytes;
+  }
+  for (int32_t w = 0; w < n_wait; ++w) {
+    const auto it = e->pending.find(engine_key(e, layer, e->h_ids[wait_idx[w]]));
+    if (it == e->pending.end()) continue;
+    MOE_HIP(hipStreamWaitEvent(e->compute, it->second, 0));
+    hipEvent_t ev = it->second;
+    e->pending.erase(it);
+    bool shared = false;
+    for (const auto &kv : e->pending) shared = shared || kv.second == ev;
+    if (!shared) e->free_events.push_back(ev);
+  }
+  // 6. slot refs to the device, then the expert block
+  MOE_HIP(hipMemcpyAsync(e->d_refs, e->h_refs, (size_t)e->k * 4, hipMemcpyHostToDevice,
+                         e->compute));
+  return moe_ffn_decode(&e->pool, &e->geom, e->d_refs, e->d_scores, x, 1, e->k, y, nullptr,
+                        e->d_ffn_ws, e->ffn_ws_bytes, e->compute);
+}
+
+int moe_engine_counters(const moe_engine *e, int64_t *out) {
+  if (!e || !out) return fail(MOE_ERR_INVALID, "NULL engine/out");
+  out[0] = e->bytes_read;
+  out[1] = e->bytes_exposed;
+  out[2] = e->recall_hit;
+  out[3] = e->recall_total;
+  out[4] = (int64_t)e->pending.size();
+  return MOE_OK;
+}
+
+}  // extern "C"

@@ -5,4 +5,5 @@
 #include "grouped.hip"
 #include "stack_decode.hip"
 #include "capi.hip"
+#include "engine.hip"
 #include "policy.cpp"

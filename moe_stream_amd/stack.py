@@ -16,6 +16,8 @@ depend on residency (slot-permutation / pool-size invariance).
 """
 from __future__ import annotations
 
+import ctypes as C
+
 import numpy as np
 import torch
 
@@ -254,7 +256,10 @@ class StreamingStack:
     def __init__(self, geom: Geometry, n_layers: int, n_slots: int, device="cuda",
                  seed: int = synth.SEED_BASE + 2, zipf_s: float | None = 1.1,
                  router_bias: bool = False, widen: int = 1, host_store=None,
-                 evict: str | None = None):
+                 evict: str | None = None, native: bool = False):
+        """native: run each layer's engine loop in the library
+        (moe_engine_layer) instead of MoEBlock.streaming_call; same policy,
+        fills and kernels, no Python frame between a layer's steps."""
         from .block import MoEBlock
         from .pool import ExpertPool
         self.geom = geom
@@ -273,15 +278,67 @@ class StreamingStack:
             self.blocks.append(MoEBlock(Lx, geom, self.pool, self.W[Lx],
                                         None if self.bias is None else self.bias[Lx],
                                         self.blocks, widen=widen))
+        self.native = native
+        self._engine = None
+        if native:
+            from .pool import HostStore
+            if not isinstance(self.store, HostStore):
+                raise ValueError("the native engine fills from a pinned host store")
+            self.k_pred = min(self.k * widen, self.E, 64)
+            self._compute = torch.cuda.current_stream(self.device)
+            h = C.c_void_p()
+            g = geom.c_geom()
+            _lib.check(_lib.lib().moe_engine_create(
+                C.byref(self.pool.c_view()), C.byref(g), n_layers, self.E, self.k,
+                self.k_pred, self.pool.policy._h, self.store.ptr, self.store.record_bytes,
+                self.store.n_records, _lib.stream_ptr(self._compute),
+                _lib.stream_ptr(self.pool.side), C.byref(h)))
+            self._engine = h
+
+    def close(self):
+        if self._engine:
+            _lib.lib().moe_engine_destroy(self._engine)
+            self._engine = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
     def token(self, x_tok: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         """x_tok: bf16 [n_layers, d_model]; returns y bf16 [n_layers, d_model]."""
         if out is None:
             out = torch.empty_like(x_tok)
+        if self._engine:
+            return self._token_native(x_tok, out)
         for Lx, blk in enumerate(self.blocks):
             out[Lx:Lx + 1] = blk(x_tok[Lx:Lx + 1])
         return out
 
+    def _token_native(self, x_tok, out):
+        assert x_tok.is_contiguous() and out.is_contiguous()
+        L, lib, g = self.L, _lib.lib(), self.geom
+        bias = self.bias
+        for Lx in range(L):
+            nxt = Lx + 1 < L
+            _lib.check(lib.moe_engine_layer(
+                self._engine, Lx, x_tok[Lx].data_ptr(), self.W[Lx].data_ptr(),
+                None if bias is None else bias[Lx].data_ptr(), g.routing,
+                int(g.norm_topk_prob), self.W[Lx + 1].data_ptr() if nxt else None,
+                None if (bias is None or not nxt) else bias[Lx + 1].data_ptr(),
+                out[Lx].data_ptr()))
+        return out
+
+    def engine_counters(self) -> dict:
+        v = (C.c_int64 * 5)()
+        _lib.check(_lib.lib().moe_engine_counters(self._engine, v))
+        return dict(bytes_read=v[0], bytes_exposed=v[1], recall_hit=v[2], recall_total=v[3],
+                    pending=v[4])
+
     def recall(self) -> float:
+        if self._engine:
+            c = self.engine_counters()
+            return c["recall_hit"] / c["recall_total"] if c["recall_total"] else float("nan")
         r = [v for b in self.blocks for v in b.recall]
         return float(np.mean(r)) if r else float("nan")
