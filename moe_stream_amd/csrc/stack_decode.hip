@@ -15,10 +15,12 @@
 //
 //   wait   : layer l-1 complete (its output is this layer's input)
 //   split  : waves 0-5 gate/up + activation for the PREDICTED expert at this
-//            workgroup's position (24 rows); wave 6 one router row (+ the
-//            lookahead row), then the lookahead ranking of layer l+1; wave 7
-//            waits for all router rows and ranks them (every workgroup
-//            redundantly, identically)
+//            workgroup's position (24 rows), and waves 0-1 one 4-row task of
+//            the two SPARE positions (lookahead ranks K, K+1; their bytes go
+//            to LDS by direct-to-LDS loads while the predicted rows compute);
+//            wave 6 one router row (+ the lookahead row), then the lookahead
+//            ranking of layer l+1; wave 7 waits for all router rows and ranks
+//            them (every workgroup redundantly, identically)
 //   fix-up : routed experts that were not predicted get gate/up now
 //   D      : down + score-weighted combine over the k routed experts, 8
 //            output rows per workgroup, wave = expert; then the staging
@@ -244,14 +246,15 @@ __device__ __forceinline__ void put_acts(uint64_t *hf, uint32_t hb, uint32_t fl)
 
 // Gate/up rows of one expert for this workgroup's 24-row block, waves
 // 0..WAVES_U-1: codes in cg/cu, scales staged in sbu_l, x staged in act_l
-// and asum_l.  Writes the bf16-rounded activations to hdst[row] (device
-// scope); ref < 0 past the store flags an error and writes zeros.
+// and asum_l.  Returns the bf16 activation of this lane's row (its wave's
+// RPSU = 4 rows go out with put_acts at hf + (row0 + wave * RPSU) / 2); an
+// out-of-range ref flags an error and yields zeros.
 template <class C>
-__device__ __forceinline__ void u_rows(const StackArgs &a, int32_t ref, int row0,
-                                       const uint4 (&cg)[C::CPLU], const uint4 (&cu)[C::CPLU],
-                                       const uint4 *act_l, const float *asum_l,
-                                       const uint4 (*sbu_l)[C::SB_U4], uint64_t *hf,
-                                       uint32_t fl) {
+__device__ __forceinline__ uint32_t u_rows(const StackArgs &a, int32_t ref, int row0,
+                                           const uint4 (&cg)[C::CPLU],
+                                           const uint4 (&cu)[C::CPLU], const uint4 *act_l,
+                                           const float *asum_l,
+                                           const uint4 (*sbu_l)[C::SB_U4]) {
   constexpr int U = C::U, NG = C::NG, SGU = C::SGU, CPLU = C::CPLU, RPSU = C::RPSU;
   constexpr int SB_U4 = C::SB_U4, NP = C::NP;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -289,60 +292,23 @@ __device__ __forceinline__ void u_rows(const StackArgs &a, int32_t ref, int row0
   } else if (lane == 0) {
     flag_error();
   }
-  // the wave's RPSU = 4 consecutive rows as two flagged entries (put_acts)
   static_assert(RPSU == 4, "four rows per wave");
-  put_acts(hf + (row0 + wave * RPSU) / 2, hb, fl);
+  return hb;
 }
 
-// One fix-up task, one whole wave: gate/up + activation of rows
-// [4b, 4b+4) of a routed expert that was not predicted (16 lanes per row, as
-// in u_rows), straight from the pool; its 4 activations go out as two
-// flagged 8-byte entries (2 bf16 + fix_flag) of `hf`, the expert's [F/2]
-// entries.  `sbw`: this wave's 64 uint4 of LDS for the rows' scales.
+// One 4-row task, one whole wave: gate/up + activation of rows [4b, 4b+4)
+// of one expert (16 lanes per row, as in u_rows) from its codes in cg/cu and
+// its rows' scales in `sbw` (LDS, 4 arrays of 16 pieces: gate S, gate B,
+// up S, up B); the 4 activations go out as two flagged 8-byte entries
+// (2 bf16 + flag) at hf + 2b of the expert's [F/2] entries (put_acts of the
+// returned activation).
 template <class C>
-__device__ __forceinline__ void fix_task(const StackArgs &a, int32_t ref, int b,
-                                         const uint4 *act_l, const float *asum_l, uint4 *sbw,
-                                         uint64_t *hf, uint32_t fl) {
-  constexpr int D = C::D_, U = C::U, NG = C::NG, SGU = C::SGU, CPLU = C::CPLU, NP = C::NP;
-  static_assert(C::RPSU == 4 && SGU == 16 && NG * 2 * 4 == 16 * 16,
-                "a task: 4 rows of 16 lanes; its scales: 4 arrays of 16 pieces");
+__device__ __forceinline__ uint32_t task_rows(const StackArgs &a, int32_t ref, bool ok, int b,
+                                          const uint4 (&cg)[C::CPLU], const uint4 (&cu)[C::CPLU],
+                                          const uint4 *sbw, const uint4 *act_l,
+                                          const float *asum_l, float gbv, float ubv) {
+  constexpr int U = C::U, NG = C::NG, SGU = C::SGU, CPLU = C::CPLU;
   const int lane = threadIdx.x & 63, uj = lane % SGU, usub = lane / SGU;
-  ref = __builtin_amdgcn_readfirstlane(ref);
-  bool ok;
-  const char *gw = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
-  const char *uw = resolve_safe(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
-  const char *gs = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok);
-  const char *gb = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok);
-  const char *us = resolve_safe(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok);
-  const char *ub = resolve_safe(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok);
-  const int row = 4 * b + usub;
-  // small loads first: lane -> scale array lane / 16, piece lane % 16 of the
-  // rows' 256-byte block; the projection biases of its row
-  const int arr = lane >> 4;
-  const char *sa = arr == 0 ? gs : arr == 1 ? gb : arr == 2 ? us : ub;
-  const uint4 sv = load16(reinterpret_cast<const uint4 *>(sa + (int64_t)(4 * b) * NG * 2) + (lane & 15));
-  float gbv = 0.f, ubv = 0.f;
-  if (C::PBIAS_) {
-    bool okb;
-    gbv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-        resolve_safe(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[row]);
-    ubv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-        resolve_safe(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[row]);
-  }
-  issue_order_fence();
-  uint4 cg[CPLU], cu[CPLU];
-  const uint4 *g4 = reinterpret_cast<const uint4 *>(gw + (int64_t)row * (D / 2));
-  const uint4 *u4 = reinterpret_cast<const uint4 *>(uw + (int64_t)row * (D / 2));
-#pragma unroll
-  for (int i = 0; i < CPLU; ++i) {
-    cg[i] = load_stream16(g4 + i * SGU + uj);
-    cu[i] = load_stream16(u4 + i * SGU + uj);
-  }
-  issue_order_fence();
-  sbw[lane] = sv;
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_wave_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   const uint16_t *sbh = reinterpret_cast<const uint16_t *>(sbw);
   constexpr int SBN = 4 * NG;   // bf16 per array: 4 rows x NG groups
   float pg = 0.f, pu = 0.f;
@@ -361,7 +327,157 @@ __device__ __forceinline__ void fix_task(const StackArgs &a, int32_t ref, int b,
   uint32_t hb = 0;
   if (ok) hb = f32_to_bf16(apply_act(a.act, pg, pu, a.alpha, a.limit));
   else if (lane == 0) flag_error();
-  put_acts(hf + 2 * b, hb, fl);
+  return hb;
+}
+
+// The register loads of one 4-row task, lane by lane: its scale piece (lane
+// -> scale array lane / 16, piece lane % 16 of the rows' 256-byte block),
+// its rows' projection biases, and its gate and up code chunks, small loads
+// first.  An out-of-range ref reads slot 0 (ok false; the task flags it).
+template <class C>
+struct TaskRegs {
+  uint4 sv, cg[C::CPLU], cu[C::CPLU];
+  float gbv, ubv;
+  bool ok;
+  __device__ __forceinline__ void load(const StackArgs &a, int32_t ref, int b) {
+    constexpr int D = C::D_, NG = C::NG, SGU = C::SGU, CPLU = C::CPLU, NP = C::NP;
+    static_assert(C::RPSU == 4 && SGU == 16 && NG * 2 * 4 == 16 * 16,
+                  "a task: 4 rows of 16 lanes; its scales: 4 arrays of 16 pieces");
+    const int lane = threadIdx.x & 63, uj = lane % SGU, usub = lane / SGU;
+    const char *gw = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
+    const char *uw = resolve_safe(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
+    const char *gs = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok);
+    const char *gb = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok);
+    const char *us = resolve_safe(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok);
+    const char *ub = resolve_safe(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok);
+    const int arr = lane >> 4, row = 4 * b + usub;
+    const char *sa = arr == 0 ? gs : arr == 1 ? gb : arr == 2 ? us : ub;
+    sv = load16(reinterpret_cast<const uint4 *>(sa + (int64_t)(4 * b) * NG * 2) + (lane & 15));
+    gbv = ubv = 0.f;
+    if (C::PBIAS_) {
+      bool okb;
+      gbv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
+          resolve_safe(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[row]);
+      ubv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
+          resolve_safe(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[row]);
+    }
+    issue_order_fence();
+    const uint4 *g4 = reinterpret_cast<const uint4 *>(gw + (int64_t)row * (D / 2)) + uj;
+    const uint4 *u4 = reinterpret_cast<const uint4 *>(uw + (int64_t)row * (D / 2)) + uj;
+#pragma unroll
+    for (int i = 0; i < CPLU; ++i) {
+      cg[i] = load_stream16(g4 + i * SGU);
+      cu[i] = load_stream16(u4 + i * SGU);
+    }
+    issue_order_fence();
+  }
+  // the task from the loaded registers; `sbw`: this wave's 64 uint4 of LDS
+  // for the rows' scales
+  __device__ __forceinline__ void run(const StackArgs &a, int32_t ref, int b,
+                                      const uint4 *act_l, const float *asum_l, uint4 *sbw,
+                                      uint64_t *hf, uint32_t fl) const {
+    sbw[threadIdx.x & 63] = sv;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_wave_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    put_acts(hf + 2 * b, task_rows<C>(a, ref, ok, b, cg, cu, sbw, act_l, asum_l, gbv, ubv), fl);
+  }
+};
+
+// LDS image of one 4-row task: pieces 0..CPLU-1 gate codes, CPLU..2CPLU-1 up
+// codes, 2CPLU the scales (the layout of TaskRegs::sv), each 64 uint4 in
+// lane order.
+template <class C>
+using TaskLds = uint4[2 * C::CPLU + 1][64];
+
+// A 4-row task's pool bytes (TaskRegs' addresses) into `sl` by
+// direct-to-LDS loads: no VGPRs; they complete in order with this wave's
+// other loads.  An out-of-range ref reads slot 0 (ok false).
+template <class C>
+__device__ __forceinline__ bool task_stage_lds(const StackArgs &a, int32_t ref, int b,
+                                               uint4 (*sl)[64]) {
+  constexpr int D = C::D_, NG = C::NG, SGU = C::SGU, CPLU = C::CPLU, NP = C::NP;
+  typedef __attribute__((address_space(3))) void lds_void;
+  const int lane = threadIdx.x & 63, uj = lane % SGU, usub = lane / SGU;
+  bool ok;
+  const char *gw = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
+  const char *uw = resolve_safe(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
+  const char *gs = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok);
+  const char *gb = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok);
+  const char *us = resolve_safe(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok);
+  const char *ub = resolve_safe(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok);
+  const int arr = lane >> 4, row = 4 * b + usub;
+  const char *sa = arr == 0 ? gs : arr == 1 ? gb : arr == 2 ? us : ub;
+  const uint4 *g4 = reinterpret_cast<const uint4 *>(gw + (int64_t)row * (D / 2)) + uj;
+  const uint4 *u4 = reinterpret_cast<const uint4 *>(uw + (int64_t)row * (D / 2)) + uj;
+  __builtin_amdgcn_global_load_lds(
+      reinterpret_cast<const uint4 *>(sa + (int64_t)(4 * b) * NG * 2) + (lane & 15),
+      (lds_void *)&sl[2 * CPLU][0], 16, 0, 0);
+#pragma unroll
+  for (int i = 0; i < CPLU; ++i) {
+    __builtin_amdgcn_global_load_lds(g4 + i * SGU, (lds_void *)&sl[i][0], 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(u4 + i * SGU, (lds_void *)&sl[CPLU + i][0], 16, 0, 0);
+  }
+  return ok;
+}
+
+// The gate/up waves' rows of the predicted expert (u_rows, when `urows`),
+// with a spare task's bytes going to LDS beside them (task_stage_lds, when
+// `spare`; returns its ok in sok).  The LDS operands are restrict pointers so
+// the compiler knows u_rows' LDS reads cannot alias the direct-to-LDS loads
+// and does not wait for those before them.
+template <class C>
+__device__ __forceinline__ uint32_t u_rows_with_spare(
+    const StackArgs &a, bool urows, int32_t uref, int row0, const uint4 (&cg)[C::CPLU],
+    const uint4 (&cu)[C::CPLU], const uint4 *__restrict__ act_l,
+    const float *__restrict__ asum_l, const uint4 (*__restrict__ sbu_l)[C::SB_U4],
+    bool spare, int32_t sref, int b, uint4 (*__restrict__ sl)[64], bool &sok) {
+  // the staged codes u_rows is about to use are awaited here, for every
+  // wave alike, so that no later wait for them also covers the spare loads
+  __builtin_amdgcn_s_waitcnt(0);
+  if (spare) sok = task_stage_lds<C>(a, sref, b, sl);
+  return urows ? u_rows<C>(a, uref, row0, cg, cu, act_l, asum_l, sbu_l) : 0u;
+}
+
+// The task from the bytes task_stage_lds put in `sl`; returns the activation
+// as task_rows.  The direct-to-LDS loads are awaited explicitly, with every
+// LDS read kept after the wait: the compiler's own wait for them is not
+// placed before all of these reads.
+template <class C>
+__device__ __forceinline__ uint32_t task_rows_lds(const StackArgs &a, int32_t ref, bool ok,
+                                                  int b, const TaskLds<C> &sl,
+                                                  const uint4 *act_l, const float *asum_l) {
+  constexpr int CPLU = C::CPLU, NP = C::NP;
+  const int lane = threadIdx.x & 63, usub = (lane & 63) / C::SGU;
+  __builtin_amdgcn_s_waitcnt(0);
+  issue_order_fence();
+  float gbv = 0.f, ubv = 0.f;
+  if (C::PBIAS_) {
+    bool okb;
+    gbv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
+        resolve_safe(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[4 * b + usub]);
+    ubv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
+        resolve_safe(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[4 * b + usub]);
+  }
+  uint4 cg[CPLU], cu[CPLU];
+#pragma unroll
+  for (int i = 0; i < CPLU; ++i) {
+    cg[i] = sl[i][lane];
+    cu[i] = sl[CPLU + i][lane];
+  }
+  return task_rows<C>(a, ref, ok, b, cg, cu, sl[2 * CPLU], act_l, asum_l, gbv, ubv);
+}
+
+// One fix-up task (a routed expert that was not predicted), straight from
+// the pool.
+template <class C>
+__device__ __forceinline__ void fix_task(const StackArgs &a, int32_t ref, int b,
+                                         const uint4 *act_l, const float *asum_l, uint4 *sbw,
+                                         uint64_t *hf, uint32_t fl) {
+  ref = __builtin_amdgcn_readfirstlane(ref);
+  TaskRegs<C> r;
+  r.load(a, ref, b);
+  r.run(a, ref, b, act_l, asum_l, sbw, hf, fl);
 }
 
 // One whole wave: the F activations of one expert (`hf`, its F/2 flagged
@@ -499,6 +615,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
   __shared__ int miss_src[K];        // i-th unstaged routed expert: fix-up slot, or -1 - spare
   __shared__ int n_miss;
   __shared__ int staged[2];          // gate/up waves done staging x (slot l & 1)
+  __shared__ TaskLds<C> spare_l[2];  // the spare tasks' bytes (waves 0 and 1)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wg = blockIdx.x;
@@ -560,6 +677,17 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       // router and ranking waves never wait for the staging
       static_assert(XIT == 1 && XU4 <= 64 * W_ROUTER && C::SIT == 1 &&
                         4 * SB_U4 <= 64 * W_ROUTER, "staging by the gate/up waves");
+      // a spare task's pool bytes (task t: 4 rows of spare t / FT, on waves
+      // 0 and 1) go to LDS by direct-to-LDS loads issued after x is staged
+      // and the gate/up waves have met (a wait for x or the meeting's release
+      // would otherwise wait for them too), so they land while the predicted
+      // rows compute
+      static_assert(kSpare * FT <= 2 * NWG, "spare tasks fit waves 0 and 1");
+      const int ts = wave * NWG + wg;
+      const bool spare = wave < 2 && ts < spare_cnt[l & 1] * FT;
+      const int32_t sref =
+          __builtin_amdgcn_readfirstlane(pred_ref[l & 1][K + min(ts / FT, kSpare - 1)]);
+      bool sok = false;
       {
         const uint4 *x4 = reinterpret_cast<const uint4 *>(a.x + (size_t)l * D);
         float s = 0.f;
@@ -577,18 +705,21 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       }
       __builtin_amdgcn_wave_barrier();
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      // gate/up of the predicted expert at this workgroup's position
-      if (wave < C::WAVES_U && upos < pcnt)
-        u_rows<C>(a, pred_ref[l & 1][upos], urow0, cg, cu, act_l, asum_l, sbu_l,
-                  a.hpred + (size_t)upos * (F / 2), layer_flag(a, l));
-      // the spare positions, spread over the grid (task t: 4 rows of spare
-      // t / FT), straight from the pool while the routing runs
-      {
-        const int t = wave * NWG + wg;
-        if (wave < C::WAVES_U && t < spare_cnt[l & 1] * FT)
-          fix_task<C>(a, pred_ref[l & 1][K + t / FT], t % FT, act_l, asum_l, hact_l[wave],
-                      a.hpred + (size_t)(K + t / FT) * (F / 2), layer_flag(a, l));
-      }
+      // gate/up of the predicted expert at this workgroup's position, then
+      // the spare task from LDS, and only then the two publishes (a store
+      // between the direct-to-LDS loads and their wait would be waited for
+      // too)
+      const bool urows = wave < C::WAVES_U && upos < pcnt;
+      const uint32_t hu = u_rows_with_spare<C>(a, urows, pred_ref[l & 1][upos], urow0, cg, cu,
+                                               act_l, asum_l, sbu_l, spare, sref, ts % FT,
+                                               spare_l[wave], sok);
+      uint32_t hs = 0;
+      if (spare) hs = task_rows_lds<C>(a, sref, sok, ts % FT, spare_l[wave], act_l, asum_l);
+      if (urows)
+        put_acts(a.hpred + (size_t)upos * (F / 2) + (urow0 + wave * C::RPSU) / 2, hu,
+                 layer_flag(a, l));
+      if (spare)
+        put_acts(a.hpred + (size_t)(K + ts / FT) * (F / 2) + 2 * (ts % FT), hs, layer_flag(a, l));
       if (wave == 0) trace_mark(a, l, TR_U_ARRIVED);
     } else if (wave == W_ROUTER) {
       // one router row (the lane partition and summation order of
@@ -719,15 +850,24 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       int32_t ref_r = 0;
       const int nsp = spare_cnt[l & 1];
       if (lane < K) {
+        // fixed trip counts, so every LDS read below issues in one batch
+        int pv[K + kSpare], sv[K];
+#pragma unroll
+        for (int p = 0; p < K + kSpare; ++p) pv[p] = P[p];
+#pragma unroll
+        for (int r = 0; r < K; ++r) sv[r] = sel_id[r];
         const int er = sel_id[lane];   // routed expert of rank `lane`
         ref_r = sel_ref[lane];
+        const int pw = lane < pcnt ? P[min(lane, K - 1)] : -1;   // predicted at position `lane`
         miss = true;
-        for (int p = 0; p < pcnt; ++p) miss = miss && (P[p] != er);
-        for (int q = 0; q < nsp; ++q)
-          if (P[K + q] == er) sp = q;    // computed at a spare position
-        const int pw = lane < pcnt ? P[lane] : -1;   // predicted expert at position `lane`
+#pragma unroll
+        for (int p = 0; p < K; ++p) miss = miss && !(p < pcnt && pv[p] == er);
+#pragma unroll
+        for (int q = 0; q < kSpare; ++q)
+          if (q < nsp && pv[K + q] == er) sp = q;    // computed at a spare position
+#pragma unroll
         for (int r = 0; r < K; ++r)
-          if (pw >= 0 && sel_id[r] == pw) { routed = true; rank_w = r; }
+          if (pw >= 0 && sv[r] == pw) { routed = true; rank_w = r; }
       }
       // unstaged routed experts (rank order): a spare's activations are
       // ready; the others (true misses) get fix-up slots
