@@ -28,6 +28,8 @@ HIPCC_FLAGS = [
     "-shared",
     # no packed fp32 instructions anywhere in device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results straight into VGPRs (no accumulator-register copies)
+    "-Xarch_device", "-mllvm=-amdgpu-mfma-vgpr-form=1",
     "-Wno-unused-command-line-argument",
 ]
 
