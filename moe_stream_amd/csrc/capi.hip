@@ -59,6 +59,33 @@ int component_bytes(const moe_geom *g, int64_t *b) {
   return np * 3;
 }
 
+// The persistent decode kernel takes slot strides, store component offsets
+// and the record size as constants of its geometry (moe::PackedLayout): the
+// pool must be the packed per-component [n_slots, *shape] arrays and the
+// store the repacked records, as the reference's pool and store are.
+int check_packed_layout(const moe_pool_view *v, const moe_geom *g) {
+  int64_t cb[MOE_MAX_COMPONENTS];
+  const int nc = component_bytes(g, cb);
+  if (nc < 0) return nc;
+  int64_t off = 0;
+  for (int c = 0; c < nc; ++c) {
+    if (v->n_slots > 0 && v->slot_bytes[c] != cb[c])
+      return fail(MOE_ERR_UNSUPPORTED,
+                  "persistent decode needs packed slots: component %d stride %lld != %lld", c,
+                  (long long)v->slot_bytes[c], (long long)cb[c]);
+    if (v->store && v->comp_offset[c] != off)
+      return fail(MOE_ERR_UNSUPPORTED,
+                  "persistent decode needs repacked records: component %d at %lld != %lld", c,
+                  (long long)v->comp_offset[c], (long long)off);
+    off += cb[c];
+  }
+  const int64_t rec = (off + 16383) / 16384 * 16384;
+  if (v->store && v->record_bytes != rec)
+    return fail(MOE_ERR_UNSUPPORTED, "persistent decode needs %lld-byte records (got %lld)",
+                (long long)rec, (long long)v->record_bytes);
+  return MOE_OK;
+}
+
 int make_pool_args(const moe_pool_view *v, const moe_geom *g, moe::PoolArgs *pa) {
   if (!v) return fail(MOE_ERR_INVALID, "pool view is NULL");
   int64_t cb[MOE_MAX_COMPONENTS];
@@ -360,6 +387,8 @@ int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_lay
     return fail(MOE_ERR_UNSUPPORTED,
                 "no persistent decode kernel for d_model=%d d_ff=%d k=%d proj_bias=%d",
                 g->d_model, g->d_ff, k, g->has_proj_bias);
+  rc = check_packed_layout(pool, g);
+  if (rc) return rc;
   if (n_layers <= 0) return fail(MOE_ERR_INVALID, "n_layers=%d", n_layers);
   if (E <= 0 || E > moe::kRouteMaxE || 2 * E > S->nwg)
     return fail(MOE_ERR_INVALID, "E=%d outside [1, %d]", E, moe::kRouteMaxE);

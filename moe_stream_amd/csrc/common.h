@@ -185,6 +185,47 @@ __device__ __forceinline__ const char *resolve_safe(const PoolArgs &pa, int c, i
   return ok ? p : (pa.n_slots > 0 ? pa.base[c] : pa.store + pa.comp_offset[c]);
 }
 
+// The packed pool layout of one geometry: per-component slot arrays
+// [n_slots, *shape] with no padding and repacked store records (components
+// back to back in (gate, up, down) x (weight, scales, biases[, bias]) order,
+// the record padded to 16 KiB pages).  Strides and offsets are constants, so
+// a kernel that requires this layout holds only the base addresses.
+template <int D, int F, bool PB>
+struct PackedLayout {
+  static constexpr int NP = PB ? 4 : 3;
+  static constexpr int64_t bytes(int c) {
+    const int proj = c / NP, part = c % NP;
+    const int64_t out = proj == 2 ? D : F, in = proj == 2 ? F : D;
+    return part == 0 ? out * in / 2 : part == 3 ? out * 2 : out * (in / 64) * 2;
+  }
+  static constexpr int64_t slot_bytes(int c) { return bytes(c); }
+  static constexpr int64_t comp_offset(int c) {
+    int64_t o = 0;
+    for (int i = 0; i < c; ++i) o += bytes(i);
+    return o;
+  }
+  static constexpr int64_t kRecordBytes = (comp_offset(3 * NP) + 16383) / 16384 * 16384;
+};
+
+// resolve() / resolve_safe() for a pool in the packed layout L.
+template <class L>
+__device__ __forceinline__ const char *resolve_packed(const PoolArgs &pa, int c, int32_t ref) {
+  if (ref >= 0) {
+    if (ref >= pa.n_slots) return nullptr;
+    return pa.base[c] + (int64_t)ref * L::slot_bytes(c);
+  }
+  int64_t r = -(int64_t)ref - 1;
+  if (pa.store == nullptr || r >= pa.n_records) return nullptr;
+  return pa.store + r * L::kRecordBytes + L::comp_offset(c);
+}
+template <class L>
+__device__ __forceinline__ const char *resolve_packed_safe(const PoolArgs &pa, int c,
+                                                           int32_t ref, bool &ok) {
+  const char *p = resolve_packed<L>(pa, c, ref);
+  ok = p != nullptr;
+  return ok ? p : (pa.n_slots > 0 ? pa.base[c] : pa.store + L::comp_offset(c));
+}
+
 __device__ __forceinline__ void flag_error() {
   __hip_atomic_store(&g_device_error, 1, __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);

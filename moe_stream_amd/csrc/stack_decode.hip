@@ -207,6 +207,7 @@ template <int D, int F, int K, bool PBIAS>
 struct StackCfg {
   static constexpr int D_ = D, F_ = F, K_ = K;
   static constexpr bool PBIAS_ = PBIAS;
+  using Layout = PackedLayout<D, F, PBIAS>;   // the pool layout the kernel requires
   static constexpr int NT = 512;                 // 8 waves
   // gate/up: SG 16 lanes per row, 4 rows per wave step, 6 waves -> 24 rows
   static constexpr int U = D / 32, NG = D / 64;
@@ -259,7 +260,7 @@ __device__ __forceinline__ uint32_t u_rows(const StackArgs &a, int32_t ref, int 
   constexpr int SB_U4 = C::SB_U4, NP = C::NP;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int uj = lane % SGU, usub = lane / SGU;
-  const bool ok = resolve(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref) != nullptr;
+  const bool ok = resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref) != nullptr;
   const int urow = row0 + wave * RPSU + usub;
   float pg = 0.f, pu = 0.f;
   if (ok) {
@@ -284,9 +285,9 @@ __device__ __forceinline__ uint32_t u_rows(const StackArgs &a, int32_t ref, int 
   if (ok) {
     if (C::PBIAS_) {
       pg += bf16_to_f32(reinterpret_cast<const uint16_t *>(
-          resolve(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref))[urow]);
+          resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref))[urow]);
       pu += bf16_to_f32(reinterpret_cast<const uint16_t *>(
-          resolve(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref))[urow]);
+          resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref))[urow]);
     }
     hb = f32_to_bf16(apply_act(a.act, pg, pu, a.alpha, a.limit));
   } else if (lane == 0) {
@@ -344,12 +345,12 @@ struct TaskRegs {
     static_assert(C::RPSU == 4 && SGU == 16 && NG * 2 * 4 == 16 * 16,
                   "a task: 4 rows of 16 lanes; its scales: 4 arrays of 16 pieces");
     const int lane = threadIdx.x & 63, uj = lane % SGU, usub = lane / SGU;
-    const char *gw = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
-    const char *uw = resolve_safe(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
-    const char *gs = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok);
-    const char *gb = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok);
-    const char *us = resolve_safe(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok);
-    const char *ub = resolve_safe(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok);
+    const char *gw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
+    const char *uw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
+    const char *gs = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok);
+    const char *gb = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok);
+    const char *us = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok);
+    const char *ub = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok);
     const int arr = lane >> 4, row = 4 * b + usub;
     const char *sa = arr == 0 ? gs : arr == 1 ? gb : arr == 2 ? us : ub;
     sv = load16(reinterpret_cast<const uint4 *>(sa + (int64_t)(4 * b) * NG * 2) + (lane & 15));
@@ -357,9 +358,9 @@ struct TaskRegs {
     if (C::PBIAS_) {
       bool okb;
       gbv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-          resolve_safe(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[row]);
+          resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[row]);
       ubv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-          resolve_safe(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[row]);
+          resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[row]);
     }
     issue_order_fence();
     const uint4 *g4 = reinterpret_cast<const uint4 *>(gw + (int64_t)row * (D / 2)) + uj;
@@ -400,12 +401,12 @@ __device__ __forceinline__ bool task_stage_lds(const StackArgs &a, int32_t ref, 
   typedef __attribute__((address_space(3))) void lds_void;
   const int lane = threadIdx.x & 63, uj = lane % SGU, usub = lane / SGU;
   bool ok;
-  const char *gw = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
-  const char *uw = resolve_safe(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
-  const char *gs = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok);
-  const char *gb = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok);
-  const char *us = resolve_safe(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok);
-  const char *ub = resolve_safe(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok);
+  const char *gw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
+  const char *uw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
+  const char *gs = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok);
+  const char *gb = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok);
+  const char *us = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok);
+  const char *ub = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok);
   const int arr = lane >> 4, row = 4 * b + usub;
   const char *sa = arr == 0 ? gs : arr == 1 ? gb : arr == 2 ? us : ub;
   const uint4 *g4 = reinterpret_cast<const uint4 *>(gw + (int64_t)row * (D / 2)) + uj;
@@ -455,9 +456,9 @@ __device__ __forceinline__ uint32_t task_rows_lds(const StackArgs &a, int32_t re
   if (C::PBIAS_) {
     bool okb;
     gbv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-        resolve_safe(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[4 * b + usub]);
+        resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[4 * b + usub]);
     ubv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-        resolve_safe(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[4 * b + usub]);
+        resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[4 * b + usub]);
   }
   uint4 cg[CPLU], cu[CPLU];
 #pragma unroll
@@ -526,12 +527,12 @@ __device__ __forceinline__ void u_load(const StackArgs &a, int32_t ref, int row0
   // clamped index.
   ref = __builtin_amdgcn_readfirstlane(ref);
   bool ok;
-  const char *gw = resolve_safe(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
-  const char *uw = resolve_safe(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
-  const char *sb[4] = {resolve_safe(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok),
-                       resolve_safe(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok),
-                       resolve_safe(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok),
-                       resolve_safe(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok)};
+  const char *gw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
+  const char *uw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
+  const char *sb[4] = {resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok),
+                       resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok),
+                       resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok),
+                       resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok)};
 #pragma unroll
   for (int it = 0; it < C::SIT; ++it) {
     const int i = min(it * NT + tid, 4 * SB_U4 - 1);
@@ -562,9 +563,9 @@ __device__ __forceinline__ void d_load(const StackArgs &a, int32_t ref, int drow
   // (unconditional loads, as in u_load)
   ref = __builtin_amdgcn_readfirstlane(ref);
   bool ok;
-  const char *dw = resolve_safe(a.pa, comp_index(PROJ_DOWN, PART_W, NP), ref, ok);
-  const char *ds = resolve_safe(a.pa, comp_index(PROJ_DOWN, PART_S, NP), ref, ok);
-  const char *db = resolve_safe(a.pa, comp_index(PROJ_DOWN, PART_B, NP), ref, ok);
+  const char *dw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_W, NP), ref, ok);
+  const char *ds = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_S, NP), ref, ok);
+  const char *db = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_B, NP), ref, ok);
 #pragma unroll
   for (int it = 0; it < C::SDIT; ++it) {
     const int i = min(it * 64 + lane, 2 * SBD_U4 - 1);
@@ -925,7 +926,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
     if (wave < K) {
       const int r = d_r, fx = d_fx;
       const int32_t dref = d_ref;
-      const char *dw = resolve(a.pa, comp_index(PROJ_DOWN, PART_W, NP), dref);
+      const char *dw = resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_W, NP), dref);
 
       uint4 *hact = hact_l[wave];
       float *hsum = hsum_l[wave];
@@ -980,7 +981,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       if (dj == 0) {
         if (PBIAS && dw != nullptr)
           p += bf16_to_f32(reinterpret_cast<const uint16_t *>(
-              resolve(a.pa, comp_index(PROJ_DOWN, PART_BIAS, NP), dref))[drow0 + dsub]);
+              resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_BIAS, NP), dref))[drow0 + dsub]);
         red_l[r][dsub] = (dw != nullptr) ? sel_sc[r] * p : 0.f;
       }
     }

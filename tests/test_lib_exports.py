@@ -65,3 +65,48 @@ def test_workspace_sizes():
     g = G.QWEN3_30B_A3B.c_geom()
     assert lib.moe_ffn_decode_workspace(C.byref(g), 1, 8) >= 8 * 768 * 2
     assert lib.moe_route_workspace(1, 128) >= 256 + 2 * 128 * 4
+
+
+def _qwen3_view(pad=0, swap_store=False):
+    """A pool view over made-up (never dereferenced) addresses: 8 packed
+    slots per component, plus a repacked store; `pad` bytes added to every
+    slot stride; `swap_store` swaps the record offsets of the gate scales
+    and biases (same size, so still a legal view)."""
+    g = G.QWEN3_30B_A3B
+    v = _lib.PoolView()
+    v.n_components, v.n_slots = len(g.components), 8
+    for i, c in enumerate(g.components):
+        v.base[i] = 0x10_0000_0000 + i * 0x1000_0000
+        v.slot_bytes[i] = c.nbytes + pad
+        v.comp_offset[i] = c.offset
+    if swap_store:
+        v.comp_offset[1], v.comp_offset[2] = v.comp_offset[2], v.comp_offset[1]
+    v.store, v.record_bytes, v.n_records = 0x20_0000_0000, g.record_bytes, 16
+    return g, v
+
+
+def _stack_call(lib, g, v):
+    return lib.moe_stack_decode(C.byref(v), C.byref(g.c_geom()), 48, 128, 8, None, None,
+                                None, 0, 1, 8, None, None, None, None, None, None, None,
+                                1, None, 0, None)
+
+
+def test_persistent_decode_requires_the_packed_pool_layout():
+    """The persistent kernel takes strides and record offsets as constants of
+    its geometry: a padded slot stride, reordered store components or another
+    record size (legal for the per-call kernels) are rejected before any
+    device work."""
+    lib = _lib.lib()
+    g, v = _qwen3_view(pad=256)
+    assert _stack_call(lib, g, v) == _lib.MOE_ERR_UNSUPPORTED
+    assert b"packed slots" in lib.moe_last_error()
+    g, v = _qwen3_view(swap_store=True)
+    assert _stack_call(lib, g, v) == _lib.MOE_ERR_UNSUPPORTED
+    assert b"repacked records" in lib.moe_last_error()
+    g, v = _qwen3_view()
+    v.record_bytes += 16384
+    assert _stack_call(lib, g, v) == _lib.MOE_ERR_UNSUPPORTED
+    assert b"-byte records" in lib.moe_last_error()
+    # the packed layout passes this check; the next argument error reports
+    g, v = _qwen3_view()
+    assert _stack_call(lib, g, v) == _lib.MOE_ERR_INVALID
