@@ -194,6 +194,11 @@ int moe_route(const uint16_t *x, int32_t T, int32_t d_model,
  * (epoch + 1) * n_layers < 2^32 (past that, MOE_ERR_INVALID); after
  * MOE_ERR_DEVICE, or to go past that bound, zero the workspace and restart
  * at 1.  A workspace serves one stack (one n_layers) at a time.
+ * The pool must be in the packed layout (the reference's, engine_v3.py:180-
+ * 206, repack.py:73-82,141): slot_bytes[c] = the component's bytes, and with
+ * a store, comp_offset[c] = the components back to back and record_bytes =
+ * their sum rounded up to 16 KiB; otherwise MOE_ERR_UNSUPPORTED (the kernel
+ * takes these as constants of its geometry).
  * This fuses the per-layer calls of streaming_call (engine_v3.py:493-609) for
  * a device-resident pool; it has no single counterpart in the reference.
  */
