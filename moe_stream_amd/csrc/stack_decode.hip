@@ -126,6 +126,12 @@ __device__ __forceinline__ uint32_t *counter(const StackArgs &a, int l, int whic
   return a.cnt + ((size_t)l * kCountersPerLayer + which) * kCounterWords;
 }
 
+// The device error word, loaded in the same batch as a poll's loads, so a
+// poll that misses costs one round trip, not a second one for this check.
+__device__ __forceinline__ int poll_error_word() {
+  return __hip_atomic_load(&g_device_error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // One whole wave: poll until the counter's sum >= target (no barrier).
 // Bounded: past the spin limit, or as soon as any workgroup has flagged an
 // error, it gives up (wrong results, never a hang).
@@ -136,17 +142,17 @@ __device__ __forceinline__ void wave_wait(const uint32_t *c, uint32_t target) {
     int v = (lane < kSub) ? (int)__hip_atomic_load(c + lane * 32, __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT)
                           : 0;
+    const int err = poll_error_word();
     v += dpp_i<kDppQuadXor1>(v);
     v += dpp_i<kDppQuadXor2>(v);
     v += dpp_i<kDppHalfMirror>(v);
     const uint32_t sum = (uint32_t)__builtin_amdgcn_readfirstlane(v);
     if (sum >= target) break;
-    __builtin_amdgcn_s_sleep(1);
-    if (++spins > kSpinLimit ||
-        __hip_atomic_load(&g_device_error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+    if (++spins > kSpinLimit || __builtin_amdgcn_readfirstlane(err)) {
       if (lane == 0) flag_error();
       break;
     }
+    __builtin_amdgcn_s_sleep(1);
   }
 }
 
@@ -161,16 +167,16 @@ __device__ __forceinline__ void get_logits(const uint64_t *slots, int n, uint32_
   while (true) {
     const uint64_t v0 = __hip_atomic_load(p0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint64_t v1 = __hip_atomic_load(p1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int err = poll_error_word();
     const bool ok = (e0 >= n || (uint32_t)(v0 >> 32) == fl) && (e1 >= n || (uint32_t)(v1 >> 32) == fl);
     z0 = __uint_as_float((uint32_t)v0);
     z1 = __uint_as_float((uint32_t)v1);
     if (__ballot(!ok) == 0) break;
-    __builtin_amdgcn_s_sleep(1);
-    if (++spins > kSpinLimit ||
-        __hip_atomic_load(&g_device_error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+    if (++spins > kSpinLimit || __builtin_amdgcn_readfirstlane(err)) {
       if (lane == 0) flag_error();
       break;
     }
+    __builtin_amdgcn_s_sleep(1);
   }
 }
 
@@ -497,18 +503,18 @@ __device__ __forceinline__ void get_acts(const uint64_t *hf, uint32_t fl, uint4 
       v[q] = __hip_atomic_load(e0 + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       v[4 + q] = __hip_atomic_load(e1 + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    const int err = poll_error_word();
     bool ok = true;
 #pragma unroll
     for (int q = 0; q < 8; ++q) ok = ok && (uint32_t)(v[q] >> 32) == fl;
     p0 = make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
     p1 = make_uint4((uint32_t)v[4], (uint32_t)v[5], (uint32_t)v[6], (uint32_t)v[7]);
     if (__ballot(!ok) == 0) break;
-    __builtin_amdgcn_s_sleep(1);
-    if (++spins > kSpinLimit ||
-        __hip_atomic_load(&g_device_error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+    if (++spins > kSpinLimit || __builtin_amdgcn_readfirstlane(err)) {
       if (lane == 0) flag_error();
       break;
     }
+    __builtin_amdgcn_s_sleep(1);
   }
 }
 
