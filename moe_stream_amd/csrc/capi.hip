@@ -155,6 +155,13 @@ size_t moe_ffn_decode_workspace(const moe_geom *g, int32_t T, int32_t k) {
   return (h + 255) & ~(size_t)255;
 }
 
+// Refs of a launch read from a device array.
+static moe::RefList device_refs(const int32_t *slot_refs) {
+  moe::RefList r{};
+  r.ptr = slot_refs;
+  return r;
+}
+
 // Shared argument checks of the decode entry points.
 static int ffn_prepare(const moe_pool_view *pool, const moe_geom *g,
                        const int32_t *slot_refs, int32_t T, int32_t k,
@@ -194,7 +201,7 @@ int moe_ffn_decode_up(const moe_pool_view *pool, const moe_geom *g,
   if (!x) return fail(MOE_ERR_INVALID, "NULL x");
   if (!aligned(x, 16)) return fail(MOE_ERR_INVALID, "x must be 16-byte aligned");
   (void)hipGetLastError();
-  moe::launch_ffn_up(L, pa, slot_refs, x, T, k, static_cast<uint16_t *>(workspace),
+  moe::launch_ffn_up(L, pa, device_refs(slot_refs), x, T, k, static_cast<uint16_t *>(workspace),
                      g->act, g->alpha, g->limit, static_cast<hipStream_t>(stream));
   MOE_HIP(hipGetLastError());
   return MOE_OK;
@@ -212,9 +219,39 @@ int moe_ffn_decode_down(const moe_pool_view *pool, const moe_geom *g,
   if (!scores) return fail(MOE_ERR_INVALID, "NULL scores");
   if (!out_bf16 && !out_f32) return fail(MOE_ERR_INVALID, "no output buffer");
   (void)hipGetLastError();
-  moe::launch_ffn_down(L, pa, slot_refs, scores, T, k,
+  moe::launch_ffn_down(L, pa, device_refs(slot_refs), scores, T, k,
                        static_cast<const uint16_t *>(workspace), out_bf16, out_f32,
                        static_cast<hipStream_t>(stream));
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+// The expert block of moe_ffn_decode.  host_refs: slot_refs is host memory
+// holding T*k <= MOE_MAX_TOPK refs, which travel in the kernel arguments.
+static int ffn_decode_impl(const moe_pool_view *pool, const moe_geom *g,
+                           const int32_t *slot_refs, bool host_refs, const float *scores,
+                           const uint16_t *x, int32_t T, int32_t k, uint16_t *out_bf16,
+                           float *out_f32, void *workspace, size_t workspace_bytes,
+                           void *stream) {
+  moe::PoolArgs pa;
+  const moe::FfnLaunch *L = nullptr;
+  int rc = ffn_prepare(pool, g, slot_refs, T, k, workspace, workspace_bytes, &pa, &L);
+  if (rc) return rc;
+  if (!scores || !x) return fail(MOE_ERR_INVALID, "NULL scores/x");
+  if (!out_bf16 && !out_f32) return fail(MOE_ERR_INVALID, "no output buffer");
+  if (!aligned(x, 16)) return fail(MOE_ERR_INVALID, "x must be 16-byte aligned");
+  moe::RefList refs = device_refs(slot_refs);
+  if (host_refs) {
+    if ((int64_t)T * k > MOE_MAX_TOPK)
+      return fail(MOE_ERR_INVALID, "T*k=%d host refs above %d", T * k, MOE_MAX_TOPK);
+    refs.ptr = nullptr;
+    for (int32_t i = 0; i < T * k; ++i) refs.inl[i] = slot_refs[i];
+  }
+  (void)hipGetLastError();
+  moe::launch_ffn_decode(L, pa, refs, scores, x, T, k,
+                         static_cast<uint16_t *>(workspace), out_bf16, out_f32,
+                         g->act, g->alpha, g->limit,
+                         static_cast<hipStream_t>(stream));
   MOE_HIP(hipGetLastError());
   return MOE_OK;
 }
@@ -224,20 +261,8 @@ int moe_ffn_decode(const moe_pool_view *pool, const moe_geom *g,
                    const uint16_t *x, int32_t T, int32_t k, uint16_t *out_bf16,
                    float *out_f32, void *workspace, size_t workspace_bytes,
                    void *stream) {
-  moe::PoolArgs pa;
-  const moe::FfnLaunch *L = nullptr;
-  int rc = ffn_prepare(pool, g, slot_refs, T, k, workspace, workspace_bytes, &pa, &L);
-  if (rc) return rc;
-  if (!scores || !x) return fail(MOE_ERR_INVALID, "NULL scores/x");
-  if (!out_bf16 && !out_f32) return fail(MOE_ERR_INVALID, "no output buffer");
-  if (!aligned(x, 16)) return fail(MOE_ERR_INVALID, "x must be 16-byte aligned");
-  (void)hipGetLastError();
-  moe::launch_ffn_decode(L, pa, slot_refs, scores, x, T, k,
-                         static_cast<uint16_t *>(workspace), out_bf16, out_f32,
-                         g->act, g->alpha, g->limit,
-                         static_cast<hipStream_t>(stream));
-  MOE_HIP(hipGetLastError());
-  return MOE_OK;
+  return ffn_decode_impl(pool, g, slot_refs, false, scores, x, T, k, out_bf16, out_f32,
+                         workspace, workspace_bytes, stream);
 }
 
 size_t moe_ffn_grouped_workspace(const moe_geom *g, int32_t T, int32_t k) {
@@ -467,13 +492,18 @@ int moe_slot_lookup(const int32_t *table, int32_t E, const int32_t *ids,
 
 namespace {
 
-// Device-to-device slot fills, one launch per batch of up to kFillBatch
-// (record, slot) pairs carried in the kernel arguments (no index upload).
-// Workgroup (pair, chunk): chunk y of the pair's record, counted over its
-// components in order, kFillChunk bytes each, copied by 16-byte loads and
-// stores.
+// Slot fills, one launch per batch of up to kFillBatch (record, slot) pairs
+// carried in the kernel arguments (no index upload).  Work item y = (pair,
+// chunk of the pair's record counted over its components in order),
+// kFillChunk bytes, copied by 16-byte loads and stores; a grid of at most
+// kFillHostGrid workgroups strides over the items when the source is pinned
+// host memory.  That bound keeps the reads in flight over the host link to
+// kFillHostGrid x 16 KiB: every read queued there delays whatever else
+// crosses it, among them the command processor's fetch of the next dispatch
+// of every other stream.  An HBM source gets one workgroup per item.
 constexpr int kFillBatch = 160;
 constexpr int64_t kFillChunk = 64 * 1024;
+constexpr int kFillHostGrid = 16;
 
 struct FillArgs {
   char *base[MOE_MAX_COMPONENTS];
@@ -488,39 +518,45 @@ struct FillArgs {
 };
 
 __global__ __launch_bounds__(256) void fill_slots_kernel(const FillArgs a) {
-  const int i = blockIdx.x, y = blockIdx.y;
-  int c = 0;
-  while (c + 1 < a.nc && y >= a.chunk0[c + 1]) ++c;
-  const int64_t off = (int64_t)(y - a.chunk0[c]) * kFillChunk;
-  const int64_t len = min(kFillChunk, a.slot_bytes[c] - off);
-  const uint4 *s = reinterpret_cast<const uint4 *>(a.src + a.rec[i] * a.record_bytes +
-                                                   a.src_offset[c] + off);
-  uint4 *d = reinterpret_cast<uint4 *>(a.base[c] + (int64_t)a.slot[i] * a.slot_bytes[c] + off);
-  const int n16 = (int)(len / 16);
-  constexpr int U = 4;
-  int j = threadIdx.x;
-  for (; j + (U - 1) * 256 < n16; j += U * 256) {
-    uint4 v[U];
+  const int chunks = a.chunk0[a.nc];
+  for (int item = blockIdx.x; item < a.n * chunks; item += gridDim.x) {
+    const int i = item / chunks, y = item % chunks;
+    int c = 0;
+    while (c + 1 < a.nc && y >= a.chunk0[c + 1]) ++c;
+    const int64_t off = (int64_t)(y - a.chunk0[c]) * kFillChunk;
+    const int64_t len = min(kFillChunk, a.slot_bytes[c] - off);
+    const uint4 *s = reinterpret_cast<const uint4 *>(a.src + a.rec[i] * a.record_bytes +
+                                                     a.src_offset[c] + off);
+    uint4 *d = reinterpret_cast<uint4 *>(a.base[c] + (int64_t)a.slot[i] * a.slot_bytes[c] + off);
+    const int n16 = (int)(len / 16);
+    constexpr int U = 4;
+    int j = threadIdx.x;
+    for (; j + (U - 1) * 256 < n16; j += U * 256) {
+      uint4 v[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = s[j + u * 256];
+      for (int u = 0; u < U; ++u) v[u] = s[j + u * 256];
 #pragma unroll
-    for (int u = 0; u < U; ++u) d[j + u * 256] = v[u];
+      for (int u = 0; u < U; ++u) d[j + u * 256] = v[u];
+    }
+    for (; j < n16; j += 256) d[j] = s[j];
   }
-  for (; j < n16; j += 256) d[j] = s[j];
 }
 
 // The address a kernel reads `p` through: device memory as is, pinned host
-// memory (hipHostMalloc) through its device mapping; nullptr for pageable
-// host memory, which only a copy engine can read.
-const char *kernel_address(const void *p) {
+// memory (hipHostMalloc) through its device mapping (*host = true); nullptr
+// for pageable host memory, which only a copy engine can read.
+const char *kernel_address(const void *p, bool *host) {
   hipPointerAttribute_t at;
+  *host = false;
   if (hipPointerGetAttributes(&at, p) != hipSuccess) {
     (void)hipGetLastError();
     return nullptr;
   }
   if (at.type == hipMemoryTypeDevice) return static_cast<const char *>(p);
-  if (at.type == hipMemoryTypeHost && at.devicePointer)
+  if (at.type == hipMemoryTypeHost && at.devicePointer) {
+    *host = true;
     return static_cast<const char *>(at.devicePointer);
+  }
   return nullptr;
 }
 
@@ -551,7 +587,8 @@ int moe_fill_slots(const moe_pool_view *pool, const void *src_store,
   // over the link: one launch per batch instead of a copy call per
   // component, whose host-side cost dominated the streaming loop) with
   // 16-byte aligned pieces; pageable memory goes through hipMemcpyAsync.
-  const char *ksrc = kernel_address(src);
+  bool host_src = false;
+  const char *ksrc = kernel_address(src, &host_src);
   bool kernel = ksrc != nullptr && aligned(ksrc, 16) && rb % 16 == 0;
   FillArgs fa{};
   int32_t chunks = 0;
@@ -575,7 +612,9 @@ int moe_fill_slots(const moe_pool_view *pool, const void *src_store,
         fa.slot[i] = dst_slots[i0 + i];
         fa.rec[i] = src_records[i0 + i];
       }
-      hipLaunchKernelGGL(fill_slots_kernel, dim3(fa.n, chunks), dim3(256), 0, s, fa);
+      const int64_t items = (int64_t)fa.n * chunks;
+      const int grid = (int)(host_src ? std::min<int64_t>(items, kFillHostGrid) : items);
+      hipLaunchKernelGGL(fill_slots_kernel, dim3(grid), dim3(256), 0, s, fa);
       MOE_HIP(hipGetLastError());
     }
     return MOE_OK;

@@ -160,6 +160,20 @@ struct PoolArgs {
   int32_t n_records;
 };
 
+// Slot references of one decode launch: a device array of T*k entries, or,
+// with ptr == nullptr, at most MOE_MAX_TOPK entries carried in the kernel
+// arguments (a host that holds the refs then launches without copying them
+// to the device first).  The index is wave-uniform, so either form is one
+// scalar load.
+struct RefList {
+  const int32_t *ptr;
+  int32_t inl[MOE_MAX_TOPK];
+  __device__ __forceinline__ int32_t operator[](int i) const {
+    if (ptr != nullptr) return __builtin_amdgcn_readfirstlane(ptr[i]);
+    return __builtin_amdgcn_readfirstlane(inl[i]);
+  }
+};
+
 // Base address of component c for a slot reference; nullptr when the
 // reference is out of range (the caller then contributes nothing and the
 // device error word is set).

@@ -2,19 +2,27 @@
 // steps of streaming_call (engine_v3.py:493-609) without a Python frame in
 // between.  Per layer, in the reference's order:
 //   1. route + one lookahead (engine_v3.py:509-515) on the compute stream;
-//   2. the layer's ids and predictions to pinned host memory, ONE host
-//      synchronisation (engine_v3.py:515);
+//   2. the router writes the layer's ids and predictions straight into
+//      coherent pinned host memory; the host waits for them there (the one
+//      host synchronisation of engine_v3.py:515, without a copy command or a
+//      stream synchronisation);
 //   3. recall bookkeeping of the previous layer's prediction (:521-523);
 //   4. prefetch of the predicted layer-(l+1) experts (:521-527, ExpertPool.
 //      prefetch :383-396): fills from the pinned host store on the side
 //      stream, one event per prefetch batch, pending until retired;
 //   5. acquire (:537-552, ExpertPool.acquire :398-454): misses filled on the
 //      compute stream, in-flight prefetches become stream waits;
-//   6. slot refs to the device (pinned host -> HBM, async) and the expert
-//      block (the decode kernels) on the compute stream.
+//   6. the expert block (the decode kernels) on the compute stream, its slot
+//      refs carried in the kernel arguments (no copy to the device).
+// Reuse of the pinned buffers is safe by stream order: the host rewrites
+// them only after it has seen the next layer's router output, and that
+// router started after the previous expert block completed.
 // The slot policy is the same native policy ExpertPool uses; the engine owns
 // the pending fills' events.
 
+#include <atomic>
+#include <chrono>
+#include <cstring>
 #include <unordered_map>
 #include <vector>
 
@@ -37,12 +45,14 @@ struct moe_engine {
   int32_t L = 0, E = 0, k = 0, kp = 0;
   hipStream_t compute = nullptr, side = nullptr;
   // device buffers
-  int32_t *d_ids = nullptr, *d_pred = nullptr, *d_refs = nullptr;
   float *d_scores = nullptr;
   void *d_route_ws = nullptr, *d_ffn_ws = nullptr;
   size_t route_ws_bytes = 0, ffn_ws_bytes = 0;
-  // pinned host staging
-  int32_t *h_ids = nullptr, *h_pred = nullptr, *h_refs = nullptr;
+  // coherent pinned host memory the router writes: host and kernel
+  // addresses of ids and predictions
+  int32_t *h_ids = nullptr, *h_pred = nullptr;
+  int32_t *k_ids = nullptr, *k_pred = nullptr;
+  int32_t h_refs[MOE_MAX_TOPK] = {};               // this layer's slot refs
   // bookkeeping
   std::unordered_map<int64_t, hipEvent_t> pending;   // key -> its fill's event
   std::vector<hipEvent_t> free_events;
@@ -90,6 +100,40 @@ int engine_poll(moe_engine *e) {
     for (hipEvent_t f : e->free_events) listed = listed || f == ev;
     if (!shared && !listed) e->free_events.push_back(ev);
   }
+  return MOE_OK;
+}
+
+// Wait for the router's ids (and predictions) in pinned memory.  Every entry
+// is -1 before the launch and is written once with an id in [0, E), so all
+// entries non-negative means the output is complete.  The stream is queried
+// only once a wait has run past 1 ms (and every 1 ms after), so that a failed
+// launch ends the wait with its error: a query on every pass of a normal
+// (~30 us) wait cost the loop 13 % of its rate.
+int engine_wait_route(moe_engine *e, bool look) {
+  using clock = std::chrono::steady_clock;
+  const volatile int32_t *ids = e->h_ids, *pred = e->h_pred;
+  auto ready = [&]() {
+    bool r = true;
+    for (int32_t i = 0; i < e->k; ++i) r = r && ids[i] >= 0;
+    for (int32_t i = 0; look && i < e->kp; ++i) r = r && pred[i] >= 0;
+    return r;
+  };
+  clock::time_point next{};
+  for (uint32_t spin = 0; !ready(); ++spin) {
+    if (spin % 1024 != 1023) continue;
+    const clock::time_point now = clock::now();
+    if (next == clock::time_point{}) {
+      next = now + std::chrono::milliseconds(1);
+      continue;
+    }
+    if (now < next) continue;
+    next = now + std::chrono::milliseconds(1);
+    const hipError_t q = hipStreamQuery(e->compute);
+    if (q == hipErrorNotReady) continue;
+    if (q != hipSuccess) return hip_fail(q, "router launch");
+    if (!ready()) return fail(MOE_ERR_INVALID, "router finished without writing its ids");
+  }
+  std::atomic_thread_fence(std::memory_order_acquire);
   return MOE_OK;
 }
 
@@ -148,15 +192,18 @@ int moe_engine_create(const moe_pool_view *pool, const moe_geom *g, int32_t n_la
     if (err == hipSuccess) err = hipMalloc(p, b);
     if (err == hipSuccess) err = hipMemset(*p, 0, b);
   };
-  dmalloc(reinterpret_cast<void **>(&e->d_ids), 256);
-  dmalloc(reinterpret_cast<void **>(&e->d_pred), 256);
-  dmalloc(reinterpret_cast<void **>(&e->d_refs), 256);
   dmalloc(reinterpret_cast<void **>(&e->d_scores), 256);
   dmalloc(&e->d_route_ws, e->route_ws_bytes);
   dmalloc(&e->d_ffn_ws, e->ffn_ws_bytes);
-  if (err == hipSuccess) err = hipHostMalloc(reinterpret_cast<void **>(&e->h_ids), 256);
-  if (err == hipSuccess) err = hipHostMalloc(reinterpret_cast<void **>(&e->h_pred), 256);
-  if (err == hipSuccess) err = hipHostMalloc(reinterpret_cast<void **>(&e->h_refs), 256);
+  auto shared = [&](int32_t **h, int32_t **k) {
+    if (err == hipSuccess)
+      err = hipHostMalloc(reinterpret_cast<void **>(h), 256,
+                          hipHostMallocMapped | hipHostMallocCoherent);
+    if (err == hipSuccess) err = hipHostGetDevicePointer(reinterpret_cast<void **>(k), *h, 0);
+    if (err == hipSuccess) memset(*h, 0xff, 256);
+  };
+  shared(&e->h_ids, &e->k_ids);
+  shared(&e->h_pred, &e->k_pred);
   if (err != hipSuccess) {
     moe_engine_destroy(e);
     return hip_fail(err, "engine buffers");
@@ -174,15 +221,11 @@ int moe_engine_destroy(moe_engine *e) {
   std::sort(evs.begin(), evs.end());
   evs.erase(std::unique(evs.begin(), evs.end()), evs.end());
   for (hipEvent_t ev : evs) (void)hipEventDestroy(ev);
-  (void)hipFree(e->d_ids);
-  (void)hipFree(e->d_pred);
-  (void)hipFree(e->d_refs);
   (void)hipFree(e->d_scores);
   (void)hipFree(e->d_route_ws);
   (void)hipFree(e->d_ffn_ws);
   (void)hipHostFree(e->h_ids);
   (void)hipHostFree(e->h_pred);
-  (void)hipHostFree(e->h_refs);
   delete e;
   return MOE_OK;
 }
@@ -194,18 +237,18 @@ int moe_engine_layer(moe_engine *e, int32_t layer, const uint16_t *x, const uint
   if (layer < 0 || layer >= e->L) return fail(MOE_ERR_INVALID, "layer %d outside [0, %d)", layer, e->L);
   if (!x || !W || !y) return fail(MOE_ERR_INVALID, "NULL x/W/y");
   const bool look = W_next != nullptr && layer + 1 < e->L;
-  // 1. route + lookahead
-  int rc = moe_route(x, 1, e->geom.d_model, W, bias, e->E, mode, renorm, e->k, e->d_ids,
+  // 1. route + lookahead, outputs into pinned memory reset to -1
+  for (int32_t i = 0; i < e->k; ++i) e->h_ids[i] = -1;
+  for (int32_t i = 0; look && i < e->kp; ++i) e->h_pred[i] = -1;
+  std::atomic_thread_fence(std::memory_order_release);
+  int rc = moe_route(x, 1, e->geom.d_model, W, bias, e->E, mode, renorm, e->k, e->k_ids,
                      e->d_scores, look ? W_next : nullptr, look ? bias_next : nullptr, e->kp,
-                     look ? e->d_pred : nullptr, nullptr, nullptr, nullptr, e->d_route_ws,
+                     look ? e->k_pred : nullptr, nullptr, nullptr, nullptr, e->d_route_ws,
                      e->route_ws_bytes, e->compute);
   if (rc) return rc;
   // 2. one host synchronisation for routing and speculation
-  MOE_HIP(hipMemcpyAsync(e->h_ids, e->d_ids, (size_t)e->k * 4, hipMemcpyDeviceToHost, e->compute));
-  if (look)
-    MOE_HIP(hipMemcpyAsync(e->h_pred, e->d_pred, (size_t)e->kp * 4, hipMemcpyDeviceToHost,
-                           e->compute));
-  MOE_HIP(hipStreamSynchronize(e->compute));
+  rc = engine_wait_route(e, look);
+  if (rc) return rc;
   // 3. recall of the prediction made for this layer
   if (e->last_pred_layer == layer) {
     int32_t hit = 0;
@@ -263,11 +306,9 @@ int moe_engine_layer(moe_engine *e, int32_t layer, const uint16_t *x, const uint
     for (const auto &kv : e->pending) shared = shared || kv.second == ev;
     if (!shared) e->free_events.push_back(ev);
   }
-  // 6. slot refs to the device, then the expert block
-  MOE_HIP(hipMemcpyAsync(e->d_refs, e->h_refs, (size_t)e->k * 4, hipMemcpyHostToDevice,
-                         e->compute));
-  return moe_ffn_decode(&e->pool, &e->geom, e->d_refs, e->d_scores, x, 1, e->k, y, nullptr,
-                        e->d_ffn_ws, e->ffn_ws_bytes, e->compute);
+  // 6. the expert block, slot refs in the kernel arguments
+  return ffn_decode_impl(&e->pool, &e->geom, e->h_refs, true, e->d_scores, x, 1, e->k, y,
+                         nullptr, e->d_ffn_ws, e->ffn_ws_bytes, e->compute);
 }
 
 int moe_engine_counters(const moe_engine *e, int64_t *out) {

@@ -81,7 +81,7 @@ __device__ __forceinline__ float apply_act(int act, float g, float u,
 // ---------------------------------------------------------------------------
 template <int D, int F, int SG, int WAVES, int RSTEPS, bool PBIAS>
 __global__ __launch_bounds__(WAVES * 64) void ffn_gate_up_kernel(
-    PoolArgs pa, const int32_t *__restrict__ refs,
+    PoolArgs pa, const RefList refs,
     const uint16_t *__restrict__ x, int k, uint16_t *__restrict__ h, int act,
     float alpha, float limit) {
   constexpr int U = D / 32;                 // 16-byte code chunks per row
@@ -250,7 +250,7 @@ struct DownLds {
 
 template <int D, int F, int SG, int RSTEPS, bool PBIAS>
 __global__ __launch_bounds__(64 * MOE_MAX_TOPK) void ffn_down_kernel(
-    PoolArgs pa, const int32_t *__restrict__ refs,
+    PoolArgs pa, const RefList refs,
     const float *__restrict__ scores, const uint16_t *__restrict__ h, int k,
     uint16_t *__restrict__ out, float *__restrict__ out32) {
   using LY = DownLds<D, F, SG, RSTEPS>;
@@ -375,14 +375,14 @@ __global__ __launch_bounds__(64 * MOE_MAX_TOPK) void ffn_down_kernel(
 // ---------------------------------------------------------------------------
 template <int D, int F, int SG, int WAVES, int RSTEPS, bool PBIAS>
 static void launch_up(dim3 g, dim3 b, hipStream_t s, const PoolArgs &pa,
-                      const int32_t *refs, const uint16_t *x, int k,
+                      const RefList &refs, const uint16_t *x, int k,
                       uint16_t *h, int act, float alpha, float limit) {
   hipLaunchKernelGGL((ffn_gate_up_kernel<D, F, SG, WAVES, RSTEPS, PBIAS>), g, b,
                      0, s, pa, refs, x, k, h, act, alpha, limit);
 }
 template <int D, int F, int SG, int RSTEPS, bool PBIAS>
 static void launch_down(dim3 g, dim3 b, hipStream_t s, const PoolArgs &pa,
-                        const int32_t *refs, const float *sc, const uint16_t *h,
+                        const RefList &refs, const float *sc, const uint16_t *h,
                         int k, uint16_t *out, float *out32) {
   const size_t lds = DownLds<D, F, SG, RSTEPS>::bytes(k);
   hipLaunchKernelGGL((ffn_down_kernel<D, F, SG, RSTEPS, PBIAS>), g, b, lds, s,
@@ -423,7 +423,7 @@ const FfnLaunch *find_ffn(int d_model, int d_ff, int has_bias) {
   return nullptr;
 }
 
-void launch_ffn_up(const FfnLaunch *L, const PoolArgs &pa, const int32_t *refs,
+void launch_ffn_up(const FfnLaunch *L, const PoolArgs &pa, const RefList &refs,
                    const uint16_t *x, int T, int k, uint16_t *h, int act,
                    float alpha, float limit, hipStream_t s) {
   dim3 g(T * k * (L->d_ff / L->up_rows_wg)), b(L->up_threads);
@@ -431,7 +431,7 @@ void launch_ffn_up(const FfnLaunch *L, const PoolArgs &pa, const int32_t *refs,
 }
 
 void launch_ffn_down(const FfnLaunch *L, const PoolArgs &pa,
-                     const int32_t *refs, const float *scores, int T, int k,
+                     const RefList &refs, const float *scores, int T, int k,
                      const uint16_t *h, uint16_t *out, float *out32,
                      hipStream_t s) {
   dim3 g(T * (L->d_model / L->down_rows_wg)), b(64 * k);
@@ -439,7 +439,7 @@ void launch_ffn_down(const FfnLaunch *L, const PoolArgs &pa,
 }
 
 void launch_ffn_decode(const FfnLaunch *L, const PoolArgs &pa,
-                       const int32_t *refs, const float *scores,
+                       const RefList &refs, const float *scores,
                        const uint16_t *x, int T, int k, uint16_t *h,
                        uint16_t *out, float *out32, int act, float alpha,
                        float limit, hipStream_t s) {

@@ -10,22 +10,22 @@ struct FfnLaunch {
   int d_model, d_ff, has_bias;
   int up_rows_wg, up_threads;  // gate/up kernel: rows and threads per WG
   int down_rows_wg;            // down kernel: output rows per WG
-  void (*up)(dim3, dim3, hipStream_t, const PoolArgs &, const int32_t *,
+  void (*up)(dim3, dim3, hipStream_t, const PoolArgs &, const RefList &,
              const uint16_t *, int, uint16_t *, int, float, float);
-  void (*down)(dim3, dim3, hipStream_t, const PoolArgs &, const int32_t *,
+  void (*down)(dim3, dim3, hipStream_t, const PoolArgs &, const RefList &,
                const float *, const uint16_t *, int, uint16_t *, float *);
   size_t (*down_lds)(int k);   // dynamic LDS bytes of the down kernel
 };
 const FfnLaunch *find_ffn(int d_model, int d_ff, int has_bias);
-void launch_ffn_up(const FfnLaunch *L, const PoolArgs &pa, const int32_t *refs,
+void launch_ffn_up(const FfnLaunch *L, const PoolArgs &pa, const RefList &refs,
                    const uint16_t *x, int T, int k, uint16_t *h, int act,
                    float alpha, float limit, hipStream_t s);
 void launch_ffn_down(const FfnLaunch *L, const PoolArgs &pa,
-                     const int32_t *refs, const float *scores, int T, int k,
+                     const RefList &refs, const float *scores, int T, int k,
                      const uint16_t *h, uint16_t *out, float *out32,
                      hipStream_t s);
 void launch_ffn_decode(const FfnLaunch *L, const PoolArgs &pa,
-                       const int32_t *refs, const float *scores,
+                       const RefList &refs, const float *scores,
                        const uint16_t *x, int T, int k, uint16_t *h,
                        uint16_t *out, float *out32, int act, float alpha,
                        float limit, hipStream_t s);

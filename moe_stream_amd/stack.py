@@ -316,18 +316,29 @@ class StreamingStack:
             out[Lx:Lx + 1] = blk(x_tok[Lx:Lx + 1])
         return out
 
+    def _layer_args(self):
+        """Per layer: (router, router bias, next router, next bias) pointers."""
+        if getattr(self, "_largs", None) is None:
+            W, b, L = self.W, self.bias, self.L
+            ptr = lambda t: None if t is None else t.data_ptr()
+            self._largs = [(W[Lx].data_ptr(), ptr(None if b is None else b[Lx]),
+                            W[Lx + 1].data_ptr() if Lx + 1 < L else None,
+                            ptr(None if (b is None or Lx + 1 >= L) else b[Lx + 1]))
+                           for Lx in range(L)]
+        return self._largs
+
     def _token_native(self, x_tok, out):
         assert x_tok.is_contiguous() and out.is_contiguous()
-        L, lib, g = self.L, _lib.lib(), self.geom
-        bias = self.bias
-        for Lx in range(L):
-            nxt = Lx + 1 < L
-            _lib.check(lib.moe_engine_layer(
-                self._engine, Lx, x_tok[Lx].data_ptr(), self.W[Lx].data_ptr(),
-                None if bias is None else bias[Lx].data_ptr(), g.routing,
-                int(g.norm_topk_prob), self.W[Lx + 1].data_ptr() if nxt else None,
-                None if (bias is None or not nxt) else bias[Lx + 1].data_ptr(),
-                out[Lx].data_ptr()))
+        assert x_tok.dtype == out.dtype == torch.bfloat16
+        assert x_tok.shape == out.shape == (self.L, self.geom.d_model)
+        step = self.geom.d_model * 2
+        layer, eng, g = _lib.lib().moe_engine_layer, self._engine, self.geom
+        mode, renorm = g.routing, int(g.norm_topk_prob)
+        x0, y0 = x_tok.data_ptr(), out.data_ptr()
+        for Lx, (w, b, wn, bn) in enumerate(self._layer_args()):
+            rc = layer(eng, Lx, x0 + Lx * step, w, b, mode, renorm, wn, bn, y0 + Lx * step)
+            if rc < 0:
+                _lib.check(rc)
         return out
 
     def engine_counters(self) -> dict:
