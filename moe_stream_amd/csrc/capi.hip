@@ -496,14 +496,17 @@ namespace {
 // carried in the kernel arguments (no index upload).  Work item y = (pair,
 // chunk of the pair's record counted over its components in order),
 // kFillChunk bytes, copied by 16-byte loads and stores; a grid of at most
-// kFillHostGrid workgroups strides over the items when the source is pinned
-// host memory.  That bound keeps the reads in flight over the host link to
-// kFillHostGrid x 16 KiB: every read queued there delays whatever else
-// crosses it, among them the command processor's fetch of the next dispatch
-// of every other stream.  An HBM source gets one workgroup per item.
+// kFillHostGrid one-wave workgroups strides over the items when the source is
+// pinned host memory.  That keeps the reads in flight over the host link to
+// 256 KiB (enough for its rate): every read queued there delays whatever
+// else crosses it, among them the command processor's fetch of the next
+// dispatch of every other stream.  One wave per workgroup spreads the fill
+// thinly over the CUs, so that no decode workgroup sharing a CU with it
+// waits long behind its outstanding loads.  An HBM source gets a 256-thread
+// workgroup per item.
 constexpr int kFillBatch = 160;
 constexpr int64_t kFillChunk = 64 * 1024;
-constexpr int kFillHostGrid = 16;
+constexpr int kFillHostGrid = 128, kFillHostThreads = 64, kFillHostLoads = 2;
 
 struct FillArgs {
   char *base[MOE_MAX_COMPONENTS];
@@ -517,7 +520,9 @@ struct FillArgs {
   int64_t rec[kFillBatch];
 };
 
-__global__ __launch_bounds__(256) void fill_slots_kernel(const FillArgs a) {
+extern "C++" {
+template <int NT, int U>
+__global__ __launch_bounds__(NT) void fill_slots_kernel(const FillArgs a) {
   const int chunks = a.chunk0[a.nc];
   for (int item = blockIdx.x; item < a.n * chunks; item += gridDim.x) {
     const int i = item / chunks, y = item % chunks;
@@ -529,18 +534,18 @@ __global__ __launch_bounds__(256) void fill_slots_kernel(const FillArgs a) {
                                                      a.src_offset[c] + off);
     uint4 *d = reinterpret_cast<uint4 *>(a.base[c] + (int64_t)a.slot[i] * a.slot_bytes[c] + off);
     const int n16 = (int)(len / 16);
-    constexpr int U = 4;
     int j = threadIdx.x;
-    for (; j + (U - 1) * 256 < n16; j += U * 256) {
+    for (; j + (U - 1) * NT < n16; j += U * NT) {
       uint4 v[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) v[u] = s[j + u * 256];
+      for (int u = 0; u < U; ++u) v[u] = s[j + u * NT];
 #pragma unroll
-      for (int u = 0; u < U; ++u) d[j + u * 256] = v[u];
+      for (int u = 0; u < U; ++u) d[j + u * NT] = v[u];
     }
-    for (; j < n16; j += 256) d[j] = s[j];
+    for (; j < n16; j += NT) d[j] = s[j];
   }
 }
+}  // extern "C++"
 
 // The address a kernel reads `p` through: device memory as is, pinned host
 // memory (hipHostMalloc) through its device mapping (*host = true); nullptr
@@ -613,8 +618,12 @@ int moe_fill_slots(const moe_pool_view *pool, const void *src_store,
         fa.rec[i] = src_records[i0 + i];
       }
       const int64_t items = (int64_t)fa.n * chunks;
-      const int grid = (int)(host_src ? std::min<int64_t>(items, kFillHostGrid) : items);
-      hipLaunchKernelGGL(fill_slots_kernel, dim3(grid), dim3(256), 0, s, fa);
+      if (host_src)
+        hipLaunchKernelGGL((fill_slots_kernel<kFillHostThreads, kFillHostLoads>),
+                           dim3((int)std::min<int64_t>(items, kFillHostGrid)),
+                           dim3(kFillHostThreads), 0, s, fa);
+      else
+        hipLaunchKernelGGL((fill_slots_kernel<256, 4>), dim3((int)items), dim3(256), 0, s, fa);
       MOE_HIP(hipGetLastError());
     }
     return MOE_OK;
