@@ -41,6 +41,26 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(uint4 a, uint4 b, f32x4_t c) {
 
 constexpr int kTileM = 64;
 
+// The bias term of one LDS pass, sum over its groups g of rowsum[row][g] *
+// C[g][n], as fp32 MFMAs of K = 4 groups: A = the row sums (lane: row l%16,
+// group l/16 of the 4-group chunk), B = this lane's feature's C of group
+// l/16 of the chunk, accumulated straight into the output tile (the layout
+// of the 16x16x32 products).  Replaces one FMA per output element and group.
+template <int GPS>
+__device__ __forceinline__ void bias_term(const float *rs_l, const float (&C)[GPS], int mb,
+                                          int col, int kq, f32x4_t &o) {
+#pragma unroll
+  for (int c = 0; c < (GPS + 3) / 4; ++c) {
+    float cb = 0.f;
+#pragma unroll
+    for (int g = 4 * c; g < (GPS < 4 * c + 4 ? GPS : 4 * c + 4); ++g)
+      if (kq == g - 4 * c) cb = C[g];
+    const int kk = 4 * c + kq;
+    const float ra = rs_l[(kk < GPS ? kk : GPS - 1) * kTileM + mb * 16 + col];
+    o = __builtin_amdgcn_mfma_f32_16x16x4f32(kk < GPS ? ra : 0.f, cb, o, 0, 0, 0);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // grouping: one workgroup of 1024 threads; hist[] in dynamic LDS spans every
 // valid slot reference, key = ref + n_records in [0, n_slots + n_records).
@@ -251,15 +271,18 @@ __global__ __launch_bounds__(256) void grouped_gate_up_kernel(
           cg = mfma16x16x32(a1, bg1, cg);
           cu = mfma16x16x32(a0, bu0, cu);
           cu = mfma16x16x32(a1, bu1, cu);
-          const float4 rs =
-              *reinterpret_cast<const float4 *>(rs_l + g * kTileM + mb * 16 + 4 * kq);
-          const float rr[4] = {rs.x, rs.y, rs.z, rs.w};
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            og[mb][r] += Sg[g] * cg[r] + Cg[g] * rr[r];
-            ou[mb][r] += Su[g] * cu[r] + Cu[g] * rr[r];
+            og[mb][r] += Sg[g] * cg[r];
+            ou[mb][r] += Su[g] * cu[r];
           }
         }
+      }
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        if (mb >= nmb) break;
+        bias_term<GPS>(rs_l, Cg, mb, col, kq, og[mb]);
+        bias_term<GPS>(rs_l, Cu, mb, col, kq, ou[mb]);
       }
     }
     float pbg = 0.f, pbu = 0.f;
@@ -351,12 +374,14 @@ __global__ __launch_bounds__(256) void grouped_down_kernel(
           f32x4_t c = {0.f, 0.f, 0.f, 0.f};
           c = mfma16x16x32(ar[0], b0, c);
           c = mfma16x16x32(ar[1], b1, c);
-          const float4 rs =
-              *reinterpret_cast<const float4 *>(rs_l + g * kTileM + mb * 16 + 4 * kq);
-          const float rr[4] = {rs.x, rs.y, rs.z, rs.w};
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o[mb][r] += S[g] * c[r] + C[g] * rr[r];
+          for (int r = 0; r < 4; ++r) o[mb][r] += S[g] * c[r];
         }
+      }
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        if (mb >= nmb) break;
+        bias_term<GPS>(rs_l, C, mb, col, kq, o[mb]);
       }
     }
     float pb = 0.f;
