@@ -226,13 +226,11 @@ int moe_ffn_decode_down(const moe_pool_view *pool, const moe_geom *g,
   return MOE_OK;
 }
 
-// The expert block of moe_ffn_decode.  host_refs: slot_refs is host memory
-// holding T*k <= MOE_MAX_TOPK refs, which travel in the kernel arguments.
-static int ffn_decode_impl(const moe_pool_view *pool, const moe_geom *g,
-                           const int32_t *slot_refs, bool host_refs, const float *scores,
-                           const uint16_t *x, int32_t T, int32_t k, uint16_t *out_bf16,
-                           float *out_f32, void *workspace, size_t workspace_bytes,
-                           void *stream) {
+int moe_ffn_decode(const moe_pool_view *pool, const moe_geom *g,
+                   const int32_t *slot_refs, const float *scores,
+                   const uint16_t *x, int32_t T, int32_t k, uint16_t *out_bf16,
+                   float *out_f32, void *workspace, size_t workspace_bytes,
+                   void *stream) {
   moe::PoolArgs pa;
   const moe::FfnLaunch *L = nullptr;
   int rc = ffn_prepare(pool, g, slot_refs, T, k, workspace, workspace_bytes, &pa, &L);
@@ -240,29 +238,13 @@ static int ffn_decode_impl(const moe_pool_view *pool, const moe_geom *g,
   if (!scores || !x) return fail(MOE_ERR_INVALID, "NULL scores/x");
   if (!out_bf16 && !out_f32) return fail(MOE_ERR_INVALID, "no output buffer");
   if (!aligned(x, 16)) return fail(MOE_ERR_INVALID, "x must be 16-byte aligned");
-  moe::RefList refs = device_refs(slot_refs);
-  if (host_refs) {
-    if ((int64_t)T * k > MOE_MAX_TOPK)
-      return fail(MOE_ERR_INVALID, "T*k=%d host refs above %d", T * k, MOE_MAX_TOPK);
-    refs.ptr = nullptr;
-    for (int32_t i = 0; i < T * k; ++i) refs.inl[i] = slot_refs[i];
-  }
   (void)hipGetLastError();
-  moe::launch_ffn_decode(L, pa, refs, scores, x, T, k,
+  moe::launch_ffn_decode(L, pa, device_refs(slot_refs), scores, x, T, k,
                          static_cast<uint16_t *>(workspace), out_bf16, out_f32,
                          g->act, g->alpha, g->limit,
                          static_cast<hipStream_t>(stream));
   MOE_HIP(hipGetLastError());
   return MOE_OK;
-}
-
-int moe_ffn_decode(const moe_pool_view *pool, const moe_geom *g,
-                   const int32_t *slot_refs, const float *scores,
-                   const uint16_t *x, int32_t T, int32_t k, uint16_t *out_bf16,
-                   float *out_f32, void *workspace, size_t workspace_bytes,
-                   void *stream) {
-  return ffn_decode_impl(pool, g, slot_refs, false, scores, x, T, k, out_bf16, out_f32,
-                         workspace, workspace_bytes, stream);
 }
 
 size_t moe_ffn_grouped_workspace(const moe_geom *g, int32_t T, int32_t k) {

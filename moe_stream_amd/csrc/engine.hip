@@ -39,6 +39,8 @@ struct PendingFill {
 struct moe_engine {
   moe_pool_view pool;
   moe_geom geom;
+  moe::PoolArgs pa;                    // kernel view of the pool, checked at creation
+  const moe::FfnLaunch *ffn = nullptr; // decode kernels for the geometry
   moe_policy *policy = nullptr;
   const char *store = nullptr;      // pinned host (or device) records
   int64_t record_bytes = 0, n_records = 0;
@@ -169,12 +171,20 @@ int moe_engine_create(const moe_pool_view *pool, const moe_geom *g, int32_t n_la
   moe::PoolArgs pa;
   const int rc = make_pool_args(pool, g, &pa);
   if (rc) return rc;
-  if (!moe::find_ffn(g->d_model, g->d_ff, g->has_proj_bias))
+  const moe::FfnLaunch *ffn = moe::find_ffn(g->d_model, g->d_ff, g->has_proj_bias);
+  if (!ffn)
     return fail(MOE_ERR_UNSUPPORTED, "no decode kernel for d_model=%d d_ff=%d", g->d_model,
                 g->d_ff);
+  if (ffn->down_lds(k) > 65536)
+    return fail(MOE_ERR_UNSUPPORTED, "k=%d needs %zu bytes of LDS in the down kernel", k,
+                ffn->down_lds(k));
+  if (g->act != MOE_ACT_SWIGLU && g->act != MOE_ACT_SWIGLU_CLAMP)
+    return fail(MOE_ERR_INVALID, "unknown activation %d", g->act);
   moe_engine *e = new moe_engine();
   e->pool = *pool;
   e->geom = *g;
+  e->pa = pa;
+  e->ffn = ffn;
   e->policy = policy;
   e->store = static_cast<const char *>(store);
   e->record_bytes = record_bytes;
@@ -306,9 +316,16 @@ int moe_engine_layer(moe_engine *e, int32_t layer, const uint16_t *x, const uint
     for (const auto &kv : e->pending) shared = shared || kv.second == ev;
     if (!shared) e->free_events.push_back(ev);
   }
-  // 6. the expert block, slot refs in the kernel arguments
-  return ffn_decode_impl(&e->pool, &e->geom, e->h_refs, true, e->d_scores, x, 1, e->k, y,
-                         nullptr, e->d_ffn_ws, e->ffn_ws_bytes, e->compute);
+  // 6. the expert block, slot refs in the kernel arguments; pool arguments
+  // and launch shapes were checked at creation, x by the router
+  moe::RefList refs{};
+  for (int32_t i = 0; i < e->k; ++i) refs.inl[i] = e->h_refs[i];
+  (void)hipGetLastError();
+  moe::launch_ffn_decode(e->ffn, e->pa, refs, e->d_scores, x, 1, e->k,
+                         static_cast<uint16_t *>(e->d_ffn_ws), y, nullptr, e->geom.act,
+                         e->geom.alpha, e->geom.limit, e->compute);
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
 }
 
 int moe_engine_counters(const moe_engine *e, int64_t *out) {
