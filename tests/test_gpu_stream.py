@@ -91,6 +91,27 @@ def test_native_engine_matches_python_loop(stacks):
     na.close()
 
 
+def test_native_engine_gptoss_equals_resident_stack():
+    """The engine loop on the gpt-oss geometry (top-4, projection biases,
+    clamped SwiGLU, biased router, top-k then softmax): the decode kernels
+    take the slot refs in their kernel arguments there too, and the outputs
+    are those of the HBM-resident stack bit for bit."""
+    geom, Lg = G.GPT_OSS_120B, 2
+    dec = DecodeStack(geom, Lg, 256, "cuda", seed=20260611, zipf_s=None, router_bias=True)
+    st = StreamingStack(geom, Lg, 16, "cuda", seed=20260611, zipf_s=None, router_bias=True,
+                        native=True)
+    xs = synth.hidden_states(5, Lg, geom.d_model, "cuda", 20260612)
+    for t in range(xs.shape[0]):
+        dec.run_token(xs[t], use_graph=False)
+        y = st.token(xs[t])
+        torch.cuda.synchronize()
+        assert torch.equal(y, dec.y), t
+    s = st.pool.stats()
+    assert s["total"] == xs.shape[0] * Lg * 4
+    assert s["miss"] > 0
+    st.close()
+
+
 def test_on_disk_store_feeds_the_pool(tmp_path):
     geom = G.SMALL
     recs = synth.make_store(geom, geom.n_layers * geom.n_experts, "cuda", 20260603)
