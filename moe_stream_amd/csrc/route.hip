@@ -64,6 +64,11 @@ __device__ void select_task(const RouteArgs &a, int task, int lane) {
   const int e0 = lane, e1 = lane + 64;
   const float *lg = a.logits + ((int64_t)(la ? 1 : 0) * a.T + t) * E;
   const uint16_t *bias = la ? a.bias_n : a.bias;
+  // the slot table entries of both candidates, loaded with the logits rather
+  // than after the selection (a dependent round trip saved); clamped indices
+  const bool tab = !la && a.table != nullptr;
+  const int32_t t0 = tab ? a.table[min(e0, E - 1)] : 0;
+  const int32_t t1 = tab ? a.table[min(e1, E - 1)] : 0;
   float z0 = -INFINITY, z1 = -INFINITY;
   if (e0 < E) {
     float l = __hip_atomic_load(lg + e0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -120,18 +125,16 @@ __device__ void select_task(const RouteArgs &a, int task, int lane) {
     a.ids[o0] = e0;
     a.scores[o0] = sc0;
     if (a.table) {
-      const int32_t ref = a.table[e0];
-      a.slot_refs[o0] = ref;
-      miss0 = ref < 0;
+      a.slot_refs[o0] = t0;
+      miss0 = t0 < 0;
     }
   }
   if (sel1) {
     a.ids[o1] = e1;
     a.scores[o1] = sc1;
     if (a.table) {
-      const int32_t ref = a.table[e1];
-      a.slot_refs[o1] = ref;
-      miss1 = ref < 0;
+      a.slot_refs[o1] = t1;
+      miss1 = t1 < 0;
     }
   }
   if (a.miss_count) {
