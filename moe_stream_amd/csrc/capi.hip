@@ -296,8 +296,10 @@ int moe_ffn_grouped(const moe_pool_view *pool, const moe_geom *g,
 
 size_t moe_route_workspace(int32_t T, int32_t E) {
   if (T <= 0 || E <= 0) return 0;
-  // counter word (padded to 256 B) + logits [2][T][E] fp32
-  return 256 + (((size_t)2 * T * E * 4 + 255) & ~(size_t)255);
+  // sequence word (padded to 256 B) + logits [2][T][E]: 8-byte flagged
+  // entries for the one-launch path (T <= 16), fp32 for many tokens
+  const size_t entry = T <= moe::kRouteMaxT ? 8 : 4;
+  return 256 + (((size_t)2 * T * E * entry + 255) & ~(size_t)255);
 }
 
 int moe_route(const uint16_t *x, int32_t T, int32_t d_model, const uint16_t *W,
@@ -347,6 +349,7 @@ int moe_route(const uint16_t *x, int32_t T, int32_t d_model, const uint16_t *W,
   a.miss_count = miss_count;
   a.counter = static_cast<uint32_t *>(workspace);
   a.logits = reinterpret_cast<float *>(static_cast<char *>(workspace) + 256);
+  a.flagged = reinterpret_cast<uint64_t *>(static_cast<char *>(workspace) + 256);
   a.T = T;
   a.D = d_model;
   a.E = E;

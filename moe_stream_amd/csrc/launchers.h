@@ -33,6 +33,7 @@ void launch_ffn_decode(const FfnLaunch *L, const PoolArgs &pa,
 // ---- router / top-k / lookahead / slot lookup (route.hip) -----------------
 constexpr int kRouteMaxE = 128;
 constexpr int kRouteMaxT = 16;
+constexpr uint32_t kRouteSpinLimit = 1u << 20;   // polls before a router wait gives up
 
 struct RouteArgs {
   const uint16_t *x;
@@ -46,8 +47,9 @@ struct RouteArgs {
   const int32_t *table;
   int32_t *slot_refs;
   int32_t *miss_count;
-  float *logits;      // [2][T][E] fp32 workspace
-  uint32_t *counter;  // workspace word, zero between launches
+  float *logits;      // [2][T][E] fp32 workspace (many tokens)
+  uint64_t *flagged;  // [2][T][E] (flag << 32 | fp32 logit) workspace (T <= kRouteMaxT)
+  uint32_t *counter;  // workspace word: the last launch's flag (T <= kRouteMaxT)
   int T, D, E, mode, renorm, k, kp;
 };
 void launch_route(const RouteArgs &a, hipStream_t s);

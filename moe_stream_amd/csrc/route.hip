@@ -2,17 +2,20 @@
 //
 // Phase 1 (every workgroup): one wave per router row computes the fp32 dot
 // x_t . W[e] for each token (bf16 pairs through v_dot2c_f32_bf16), all of
-// the row's 16-byte loads issued before any arithmetic, and stores it to the
-// workspace.  Rows 0..E-1 are this layer's router, rows E..2E-1 the next
-// layer's router (lookahead), when present.
-// Phase 2 (the last workgroup to finish, found with one relaxed device-scope
-// counter increment per workgroup after its logits stores have completed):
-// one wave per (token, router|lookahead) task turns
-// the logits into bf16 logits, softmax and ranking entirely in registers --
-// two experts per lane, DPP reductions, and a ballot radix-select of the top
-// k over order-preserving 16-bit keys -- then writes ids, scores, lookahead
-// ids and the slot-table lookup.  The counter is returned to zero by that
-// workgroup, so the workspace needs zeroing only once.
+// the row's 16-byte loads issued before any arithmetic, and publishes it as
+// an 8-byte device-scope entry (this launch's flag, fp32 logit).  Rows
+// 0..E-1 are this layer's router, rows E..2E-1 the next layer's router
+// (lookahead), when present.
+// Phase 2 (workgroup 0, after its own rows): one wave per (token,
+// router|lookahead) task polls that task's E entries until all carry the
+// launch's flag, then turns the logits into bf16 logits, softmax and ranking
+// entirely in registers -- two experts per lane, DPP reductions, k rounds of
+// a packed (order-preserving 16-bit key, inverted id) integer wave max --
+// and writes ids, scores, lookahead ids and the slot-table lookup.  The
+// flag is the workspace's sequence word + 1; workgroup 0 stores it back
+// once it has seen every entry, so the workspace needs zeroing only once.
+// Workgroup 0 waits only for workgroups dispatched after it, which never
+// wait for anything, and its polls are bounded (device error word).
 // Many tokens (prefill, T > 16): the logits come from a bf16 MFMA kernel and a
 // second kernel runs the same per-task selection.
 //
@@ -57,29 +60,35 @@ __device__ void select_topk(int key0, int key1, int kk, int lane, bool &sel0,
 // slot refs, misses), task >= T token t's lookahead prediction.  The logits
 // are read with device-scope loads: in route_kernel another workgroup of the
 // same launch wrote them.
-__device__ void select_task(const RouteArgs &a, int task, int lane) {
+// Per-task inputs loaded before the logits arrive: the bias and slot table
+// entries of both candidates (clamped indices, unconditional loads).
+struct TaskPre {
+  float b0, b1;
+  int32_t t0, t1;
+};
+__device__ __forceinline__ TaskPre task_pre(const RouteArgs &a, int task, int lane) {
+  const bool la = task >= a.T;
+  const int E = a.E, e0 = min(lane, E - 1), e1 = min(lane + 64, E - 1);
+  const uint16_t *bias = la ? a.bias_n : a.bias;
+  const bool tab = !la && a.table != nullptr;
+  TaskPre p;
+  p.b0 = bias ? bf16_to_f32(bias[e0]) : 0.f;
+  p.b1 = bias ? bf16_to_f32(bias[e1]) : 0.f;
+  p.t0 = tab ? a.table[e0] : 0;
+  p.t1 = tab ? a.table[e1] : 0;
+  return p;
+}
+
+// l0, l1: the raw router logits of experts lane and lane + 64.
+__device__ void select_task(const RouteArgs &a, int task, int lane, const TaskPre &p,
+                            float l0, float l1) {
   const int E = a.E;
   const int t = task % a.T;
   const bool la = task >= a.T;
   const int e0 = lane, e1 = lane + 64;
-  const float *lg = a.logits + ((int64_t)(la ? 1 : 0) * a.T + t) * E;
-  const uint16_t *bias = la ? a.bias_n : a.bias;
-  // the slot table entries of both candidates, loaded with the logits rather
-  // than after the selection (a dependent round trip saved); clamped indices
-  const bool tab = !la && a.table != nullptr;
-  const int32_t t0 = tab ? a.table[min(e0, E - 1)] : 0;
-  const int32_t t1 = tab ? a.table[min(e1, E - 1)] : 0;
-  float z0 = -INFINITY, z1 = -INFINITY;
-  if (e0 < E) {
-    float l = __hip_atomic_load(lg + e0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (bias) l += bf16_to_f32(bias[e0]);
-    z0 = round_bf16(l);
-  }
-  if (e1 < E) {
-    float l = __hip_atomic_load(lg + e1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (bias) l += bf16_to_f32(bias[e1]);
-    z1 = round_bf16(l);
-  }
+  const int32_t t0 = p.t0, t1 = p.t1;
+  const float z0 = e0 < E ? round_bf16(l0 + p.b0) : -INFINITY;
+  const float z1 = e1 < E ? round_bf16(l1 + p.b1) : -INFINITY;
   // ranked quantity: bf16 softmax probabilities (SOFTMAX_TOPK router) or
   // the bf16 logits (TOPK_SOFTMAX router, and every lookahead)
   float v0 = z0, v1 = z1;
@@ -144,7 +153,8 @@ __device__ void select_task(const RouteArgs &a, int task, int lane) {
 }
 
 template <int NIT>
-__device__ __forceinline__ void router_rows(const RouteArgs &a, int row, int lane) {
+__device__ __forceinline__ void router_rows(const RouteArgs &a, int row, int lane,
+                                            uint32_t fl) {
   const bool nxt = row >= a.E;
   const int e = nxt ? row - a.E : row;
   const int n8 = a.D / 8;
@@ -172,40 +182,64 @@ __device__ __forceinline__ void router_rows(const RouteArgs &a, int row, int lan
       acc = dot2_bf16(w[it].w, v[it].w, acc);
     }
     acc = group_sum<64>(acc);
-    // device-scope store: read back by the last workgroup on another CU/XCD
+    // device-scope store of (flag, logit): read by workgroup 0 on another
+    // CU/XCD, whose poll of the entry is its load
     if (lane == 0)
-      __hip_atomic_store(&a.logits[((nxt ? 1 : 0) * a.T + t) * a.E + e], acc,
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&a.flagged[((nxt ? 1 : 0) * a.T + t) * a.E + e],
+                         ((uint64_t)fl << 32) | __float_as_uint(acc), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Workgroup 0's wait for one task's E flagged logits: device-scope loads of
+// both entries of every lane until all carry this launch's flag; bounded,
+// a timeout sets the device error word.
+__device__ __forceinline__ void poll_logits(const uint64_t *lg, int E, uint32_t fl, int lane,
+                                            float &l0, float &l1) {
+  const int e0 = min(lane, E - 1), e1 = min(lane + 64, E - 1);
+  for (uint32_t spins = 0;; ++spins) {
+    const uint64_t v0 = __hip_atomic_load(lg + e0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t v1 = __hip_atomic_load(lg + e1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    l0 = __uint_as_float((uint32_t)v0);
+    l1 = __uint_as_float((uint32_t)v1);
+    const bool ok = (uint32_t)(v0 >> 32) == fl && (uint32_t)(v1 >> 32) == fl;
+    if (__all(ok)) return;
+    if (spins > kRouteSpinLimit) {
+      if (lane == 0) flag_error();
+      return;
+    }
+    __builtin_amdgcn_s_sleep(1);
   }
 }
 
 template <int NIT>
 __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // this launch's flag: the workspace's sequence word + 1.  Workgroup 0
+  // stores it back only after it has seen every row's entry, and every
+  // writer reads the word before it writes, so all writers agree.
+  const uint32_t fl =
+      __hip_atomic_load(a.counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
   const int nrows = a.E * (a.Wn ? 2 : 1);
   const int row = blockIdx.x * 4 + wave;
-  if (row < nrows) router_rows<NIT>(a, row, lane);
+  if (row < nrows) router_rows<NIT>(a, row, lane, fl);
+  if (blockIdx.x != 0) return;
 
-  // ---- the last workgroup to finish does the selection ------------------
-  // The logits travel through device-scope (sc1) stores and loads, coherent
-  // across XCDs without L2 writeback/invalidate; every wave waits for its
-  // stores to complete before the workgroup's one relaxed increment.
-  __shared__ int s_last;
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == gridDim.x - 1);
+  // ---- workgroup 0 ranks: one wave per (token, router|lookahead) task ----
+  // The logits travel as flagged device-scope (sc1) entries, coherent across
+  // XCDs without L2 writeback/invalidate; the poll of an entry is its load.
+  const int ntask = a.T * (a.Wn ? 2 : 1);
+  for (int task = wave; task < ntask; task += 4) {
+    const TaskPre p = task_pre(a, task, lane);
+    const bool la = task >= a.T;
+    float l0, l1;
+    poll_logits(a.flagged + ((int64_t)(la ? 1 : 0) * a.T + task % a.T) * a.E, a.E, fl, lane,
+                l0, l1);
+    select_task(a, task, lane, p, l0, l1);
   }
   __syncthreads();
-  if (!s_last) return;
-
-  const int ntask = a.T * (a.Wn ? 2 : 1);
-  for (int task = wave; task < ntask; task += 4) select_task(a, task, lane);
-  __syncthreads();
   if (threadIdx.x == 0)
-    __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.counter, fl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -267,8 +301,12 @@ __global__ __launch_bounds__(256) void route_logits_mfma_kernel(RouteArgs a) {
 
 // one wave per selection task, after route_logits_mfma_kernel
 __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
-  const int task = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (task < a.T * (a.Wn ? 2 : 1)) select_task(a, task, threadIdx.x & 63);
+  const int task = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (task >= a.T * (a.Wn ? 2 : 1)) return;
+  const TaskPre p = task_pre(a, task, lane);
+  const float *lg = a.logits + ((int64_t)(task >= a.T ? 1 : 0) * a.T + task % a.T) * a.E;
+  const float l0 = lg[min(lane, a.E - 1)], l1 = lg[min(lane + 64, a.E - 1)];
+  select_task(a, task, lane, p, l0, l1);
 }
 
 __global__ void slot_lookup_kernel(const int32_t *table, int E,
