@@ -41,6 +41,26 @@ def test_persistent_equals_per_layer(stack):
     assert int(stack.p_miss.sum()) > 0          # some experts read from the store
 
 
+def test_graph_replays_equal_eager(stack):
+    """The per-layer launches captured once as a HIP graph and replayed for
+    several tokens, with eager work of the same stack between the replays:
+    every replay routes and computes exactly what the eager launches do (the
+    router's per-launch sequence word advances inside the graph too)."""
+    xs = synth.hidden_states(4, stack.L, 2048, "cuda", 20260604)
+    stack.capture()
+    for t in range(xs.shape[0]):
+        stack.run_token(xs[t], use_graph=False)
+        torch.cuda.synchronize()
+        ref = stack.routed(), stack.y.clone()
+        stack.run_token(xs[t], use_graph=True)
+        torch.cuda.synchronize()
+        ops.check_device_error()
+        got = stack.routed()
+        for a, b in zip(got, ref[0]):
+            np.testing.assert_array_equal(a, b)
+        assert torch.equal(stack.y, ref[1]), t
+
+
 def test_persistent_layer_against_oracle(stack):
     xs = synth.hidden_states(1, stack.L, 2048, "cuda", 20260603)
     stack.token_persistent(xs[0])
