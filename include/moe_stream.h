@@ -168,7 +168,9 @@ int moe_ffn_grouped(const moe_pool_view *pool, const moe_geom *g,
  *   *miss_count (if not NULL) is incremented by the number of refs < 0.
  * scores are fp32 holding bf16-representable values.
  * workspace: at least moe_route_workspace() bytes, zeroed once before first
- * use (the kernel leaves its counter at zero when it returns).
+ * use (for T <= 16 it holds a sequence word the kernel advances by one per
+ * launch and the router logits as entries tagged with it, so no clearing is
+ * needed between launches).
  */
 size_t moe_route_workspace(int32_t T, int32_t E);
 int moe_route(const uint16_t *x, int32_t T, int32_t d_model,
