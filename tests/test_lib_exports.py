@@ -64,7 +64,14 @@ def test_workspace_sizes():
     lib = _lib.lib()
     g = G.QWEN3_30B_A3B.c_geom()
     assert lib.moe_ffn_decode_workspace(C.byref(g), 1, 8) >= 8 * 768 * 2
-    assert lib.moe_route_workspace(1, 128) >= 256 + 2 * 128 * 4
+    # up to 16 tokens: a sequence word + (flag, logit) 8-byte entries for the
+    # router and the lookahead; more tokens: fp32 logits
+    assert lib.moe_route_workspace(1, 128) >= 256 + 2 * 128 * 8
+    assert lib.moe_route_workspace(16, 128) >= 256 + 2 * 16 * 128 * 8
+    assert lib.moe_route_workspace(17, 128) >= 256 + 2 * 17 * 128 * 4
+    for T in (1, 5, 16, 17, 512):
+        assert lib.moe_route_workspace(T, 128) % 256 == 0
+    assert lib.moe_route_workspace(0, 128) == 0
 
 
 def _qwen3_view(pad=0, swap_store=False):
