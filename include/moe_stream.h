@@ -201,6 +201,11 @@ int moe_route(const uint16_t *x, int32_t T, int32_t d_model,
  * a store, comp_offset[c] = the components back to back and record_bytes =
  * their sum rounded up to 16 KiB; otherwise MOE_ERR_UNSUPPORTED (the kernel
  * takes these as constants of its geometry).
+ * One workgroup per CU, all resident at once: when the kernel's occupancy
+ * allows that on the device it is an ordinary launch, which expects the CUs
+ * not to be held by other kernels meanwhile (its waits are bounded: a
+ * concurrent kernel holding CUs past them yields MOE_ERR_DEVICE, not a
+ * hang); otherwise a cooperative launch.
  * This fuses the per-layer calls of streaming_call (engine_v3.py:493-609) for
  * a device-resident pool; it has no single counterpart in the reference.
  */
