@@ -43,7 +43,12 @@ def parse():
                          "measurements, not the headline)")
     ap.add_argument("--mode", default="persistent", choices=["persistent", "graph", "eager"],
                     help="persistent: one launch per token; graph/eager: 3 launches per layer")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--launch", default="ordinary", choices=["ordinary", "cooperative"],
+                    help="persistent mode: the bench owns the GPU, so an ordinary launch "
+                         "(checked after the timed steps; if a launch timed out the steps "
+                         "are measured again with cooperative launches)")
+    ap.add_argument("--cpu-repeats", type=int, default=96,
+                    help="timed layer-blocks of the CPU baseline (>= 60)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--engine", default="native", choices=["native", "python"],
                     help="qwen3-stream: the per-layer engine loop in the library "
@@ -329,59 +334,81 @@ def time_dominant_kernel(stack, xs, n_tok):
     return float(np.mean(ms)), float(np.median(ms)), len(ms)
 
 
-def cpu_baseline(stack, xs, seconds):
-    """The oracle (numpy port of the reference graph) on the host cores:
-    router + top-k + the k-expert block per layer, fp64, BLAS held to one
-    thread.  Bounded sample: consecutive layers of the first tokens until
-    `seconds` of work; rate scaled to tokens/s of the full stack."""
+def cpu_baseline(stack, xs, repeats, gpu_token=None):
+    """The expert path on the host cores: oracle.cpu_block, a torch CPU
+    restatement of the reference graph (router + top-k + the k-expert block,
+    dequantise then fp32 matrix-vector products, MLX's bf16 rounding points;
+    not MLX, which is not installed), on every visible core.
+
+    `repeats` layer-blocks of the same stack, walking the layers of
+    consecutive tokens (so the routed experts change from repeat to repeat),
+    each timed on its own; median and p10/p90 over them, after 3 warm-up
+    repeats.  The experts a repeat routes to are read from the store before
+    its timer starts (the reference's pool holds them resident).  With
+    `gpu_token(t)`, one GPU token runs before every CPU repeat, its launch
+    timed by events, so the two arms interleave."""
     import torch
-    from threadpoolctl import threadpool_limits
+    from oracle import cpu_block as CB
     from oracle import layout as OL
-    from oracle import numerics as N
     g = stack.geom
-    kind = "qwen3" if not g.has_proj_bias else "gptoss"
-    W = stack.W.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
-    B = None if stack.bias is None else stack.bias.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
-    xh = xs.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    kind = "gptoss" if g.has_proj_bias else "qwen3"
+    W = stack.W.float().cpu()
+    B = None if stack.bias is None else stack.bias.float().cpu()
+    xh = xs.float().cpu()
     cache = {}
 
     def expert(Lx, e):
         key = (Lx, e)
         if key not in cache:
+            if len(cache) >= 64:
+                cache.pop(next(iter(cache)))
             rec = stack.store[Lx * stack.E + e].cpu().numpy()
-            cache[key] = OL.split_record(rec, g.d_model, g.d_ff, g.has_proj_bias)
+            cache[key] = CB.Expert(OL.split_record(rec, g.d_model, g.d_ff, g.has_proj_bias))
         return cache[key]
 
-    done, t_work = 0, 0.0
-    with threadpool_limits(limits=1):
-        t, Lx = 0, 0
-        while t_work < seconds and done < 4 * stack.L:
-            x = N.bf16_bits_to_f32(xh[t, Lx]).astype(np.float64)
-            exps = None
-            # fetch the routed experts' bytes first (not timed: the reference
-            # reads them from its resident pool)
-            z0 = N.router_logits(x, W[Lx], None if B is None else B[Lx], "mlx")
-            ids0 = (N.top_k_experts(z0, g.top_k, g.norm_topk_prob, "mlx")[0]
-                    if g.routing == 0 else N.top_k_route(z0, g.top_k, "mlx")[0])
-            exps = [expert(Lx, int(e)) for e in ids0]
-            t0 = time.perf_counter()
-            z = N.router_logits(x, W[Lx], None if B is None else B[Lx], "mlx")
-            if g.routing == 0:
-                ids, sc, _ = N.top_k_experts(z, g.top_k, g.norm_topk_prob, "mlx")
-            else:
-                ids, sc, _ = N.top_k_route(z, g.top_k, "mlx")
-            N.moe_block(x, exps, sc, kind=kind, mode="mlx")
-            t_work += time.perf_counter() - t0
-            done += 1
-            Lx += 1
-            if Lx == stack.L:
-                Lx, t = 0, t + 1
-    per_layer = t_work / done
-    return {"value": 1.0 / (per_layer * stack.L), "unit": "tok/s", "cores": 1,
-            "kind": "port",
-            "sample": f"{done} layer-blocks (router+top-k+{g.top_k} experts, numpy fp64 "
-                      f"MLX-emulation oracle, BLAS 1 thread) of the same stack, "
-                      f"{t_work:.1f} s of CPU work; host has {os.cpu_count()} cpus"}
+    cpu_ms, gpu_us = [], []
+    warm = 3
+    for r in range(repeats + warm):
+        t, Lx = divmod(r, stack.L)
+        t %= xh.shape[0]
+        x = xh[t, Lx]
+        b = None if B is None else B[Lx]
+        ids, _ = CB.route(x, W[Lx], b, g.top_k, g.routing, g.norm_topk_prob)
+        for e in ids.tolist():          # resident before the timer starts
+            expert(Lx, e)
+        if gpu_token is not None:
+            us = gpu_token(t)
+            if r >= warm:
+                gpu_us.append(us)
+        t0 = time.perf_counter()
+        CB.moe_layer(x, W[Lx], b, lambda e: cache[(Lx, e)], g.top_k, g.routing,
+                     g.norm_topk_prob, kind, g.alpha, g.limit)
+        if r >= warm:
+            cpu_ms.append((time.perf_counter() - t0) * 1e3)
+    ms = np.array(cpu_ms)
+    p10, med, p90 = np.percentile(ms, [10, 50, 90])
+
+    def tok_s(layer_ms):
+        return round(1e3 / (layer_ms * stack.L), 3)
+    out = {"value": tok_s(med), "unit": "tok/s",
+           "cores": threads, "kind": "port",
+           "label": "CPU restatement (not MLX): torch on the host cores",
+           "os_cpu_count": os.cpu_count(), "sched_affinity": threads,
+           "torch_threads": torch.get_num_threads(),
+           "layer_ms": {"median": round(med, 3), "p10": round(p10, 3), "p90": round(p90, 3)},
+           "tok_s_p10_p90": [tok_s(p90), tok_s(p10)],
+           "repeats": len(ms),
+           "sample": f"{len(ms)} layer-blocks (router + top-k + {g.top_k} experts) of the "
+                     f"same {stack.L}-layer stack, consecutive layers of "
+                     f"{(repeats + warm - 1) // stack.L + 1} tokens, {warm} warm-up repeats; "
+                     f"tok/s = 1 / ({stack.L} x median layer time)"}
+    if gpu_us:
+        q = np.percentile(np.array(gpu_us), [10, 50, 90])
+        out["gpu_interleaved_us_per_token"] = {"median": round(q[1], 2), "p10": round(q[0], 2),
+                                               "p90": round(q[2], 2), "n": len(gpu_us)}
+    return out
 
 
 def main():
@@ -410,6 +437,7 @@ def main():
         stack.capture()
     torch.cuda.synchronize()
     launch_ev = []          # (start, end) events around every persistent launch
+    ordinary = args.launch == "ordinary"
 
     def step(timed=False):
         for t in range(args.tokens):
@@ -417,33 +445,48 @@ def main():
                 if timed:
                     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                     a.record()
-                    stack.token_persistent(xs[t])
+                    stack.token_persistent(xs[t], ordinary=ordinary)
                     b.record()
                     launch_ev.append((a, b))
                 else:
-                    stack.token_persistent(xs[t])
+                    stack.token_persistent(xs[t], ordinary=ordinary)
             else:
                 stack.run_token(xs[t], mode == "graph")
 
-    for _ in range(args.warmup):
-        step()
-    for b in stack.bufs:
-        b.miss.zero_()
+    def measure():
+        for _ in range(args.warmup):
+            step()
+        for b in stack.bufs:
+            b.miss.zero_()
+        if mode == "persistent":
+            stack.p_miss.zero_()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(args.steps):
+            step(timed=True)
+        e1.record()
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0, e0.elapsed_time(e1)
+
+    wall, gpu_ms = measure()
+    from moe_stream_amd import _lib, ops
+    launch_note = None
     if mode == "persistent":
-        stack.p_miss.zero_()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record()
-    for _ in range(args.steps):
-        step(timed=True)
-    e1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    gpu_ms = e0.elapsed_time(e1)
+        try:
+            stack.check_persistent()
+        except _lib.MoeError as e:
+            if e.code != _lib.MOE_ERR_TIMEOUT or not ordinary:
+                raise
+            # another kernel held CUs: measure again with cooperative launches
+            launch_note = "ordinary launch timed out; measured with cooperative launches"
+            ordinary = False
+            launch_ev.clear()
+            wall, gpu_ms = measure()
+            stack.check_persistent()
     ms_per_step = gpu_ms / args.steps
     tok_s = args.tokens * args.steps / (gpu_ms / 1e3)
-    from moe_stream_amd import ops
     ops.check_device_error()
     if mode == "persistent":
         misses = int(stack.p_miss.sum().item())
@@ -451,9 +494,12 @@ def main():
         misses = int(sum(int(b.miss.item()) for b in stack.bufs))
     lookups = args.steps * args.tokens * stack.L * stack.k
     cfg["pool_hit_rate"] = round(1.0 - misses / lookups, 4)
-    cfg["launch"] = {"persistent": "one cooperative launch per token (all layers)",
+    cfg["launch"] = {"persistent": ("one ordinary launch per token (all layers)" if ordinary
+                                    else "one cooperative launch per token (all layers)"),
                      "graph": "one HIP graph per token, 3 launches per layer",
                      "eager": "3 launches per layer"}[mode]
+    if launch_note:
+        cfg["launch_note"] = launch_note
     cfg["parallelism"] = "none (1 GPU)"
     cfg["seq_len"] = 1
 
@@ -491,7 +537,21 @@ def main():
            "stack_expert_GBs": round(block_bytes * tok_s / 1e9, 1),
            "wall_s": round(wall, 3)}
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(stack, xs, args.cpu_seconds)
+        gs = torch.cuda.current_stream()
+
+        def gpu_token(t):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(gs)
+            if mode == "persistent":
+                stack.token_persistent(xs[t], ordinary=ordinary)
+            else:
+                stack.run_token(xs[t], mode == "graph")
+            b.record(gs)
+            b.synchronize()
+            return a.elapsed_time(b) * 1e3
+        out["cpu_baseline"] = cpu_baseline(stack, xs, max(60, args.cpu_repeats), gpu_token)
+        if mode == "persistent":
+            stack.check_persistent()
     print(json.dumps(out), flush=True)
 
 

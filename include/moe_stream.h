@@ -28,7 +28,11 @@ enum {
   MOE_ERR_UNSUPPORTED = -2, /* geometry with no compiled kernel            */
   MOE_ERR_HIP = -3,         /* the HIP runtime reported an error           */
   MOE_ERR_EXHAUSTED = -4,   /* slot pool exhausted (every slot pinned)     */
-  MOE_ERR_DEVICE = -5       /* a kernel flagged an out-of-range slot ref   */
+  MOE_ERR_DEVICE = -5,      /* a kernel flagged an out-of-range slot ref   */
+  MOE_ERR_TIMEOUT = -6      /* a kernel's bounded wait for another workgroup
+                               gave up (moe_stack_decode with
+                               MOE_STACK_ORDINARY whose grid was not resident
+                               at once); that launch's outputs are invalid  */
 };
 
 /* Gated activation between gate/up and down. */
@@ -182,8 +186,14 @@ int moe_route(const uint16_t *x, int32_t T, int32_t d_model,
               const int32_t *table, int32_t *slot_refs, int32_t *miss_count,
               void *workspace, size_t workspace_bytes, void *stream);
 
+/* moe_stack_decode flags */
+enum {
+  MOE_STACK_COOPERATIVE = 0, /* default: a cooperative launch                  */
+  MOE_STACK_ORDINARY = 1     /* an ordinary launch (see below)                  */
+};
+
 /*
- * Whole-token decode of an n_layers stack in ONE cooperative launch: for
+ * Whole-token decode of an n_layers stack in ONE launch: for
  * each layer l, route x[l] with W[l] (+ bias[l]) and look ahead with W[l+1],
  * look the routed experts up in table[l] (slot refs, as moe_route), run the
  * expert block, write y[l].  Per-layer outputs: ids/scores/slot_refs
@@ -194,18 +204,24 @@ int moe_route(const uint16_t *x, int32_t T, int32_t d_model,
  * only after y[l] is complete.
  * epoch: 1 for the first launch on a zeroed workspace, then 2, 3, ... while
  * (epoch + 1) * n_layers < 2^32 (past that, MOE_ERR_INVALID); after
- * MOE_ERR_DEVICE, or to go past that bound, zero the workspace and restart
- * at 1.  A workspace serves one stack (one n_layers) at a time.
+ * MOE_ERR_DEVICE or MOE_ERR_TIMEOUT, or to go past that bound, zero the
+ * workspace and restart at 1.  A workspace serves one stack (one n_layers)
+ * at a time.
  * The pool must be in the packed layout (the reference's, engine_v3.py:180-
  * 206, repack.py:73-82,141): slot_bytes[c] = the component's bytes, and with
  * a store, comp_offset[c] = the components back to back and record_bytes =
  * their sum rounded up to 16 KiB; otherwise MOE_ERR_UNSUPPORTED (the kernel
  * takes these as constants of its geometry).
- * One workgroup per CU, all resident at once: when the kernel's occupancy
- * allows that on the device it is an ordinary launch, which expects the CUs
- * not to be held by other kernels meanwhile (its waits are bounded: a
- * concurrent kernel holding CUs past them yields MOE_ERR_DEVICE, not a
- * hang); otherwise a cooperative launch.
+ * One workgroup per CU, all resident at once, each waiting for the others.
+ * flags = MOE_STACK_COOPERATIVE: a cooperative launch, which guarantees
+ * that.  flags = MOE_STACK_ORDINARY: an ordinary launch (~16 us less
+ * dispatch cost per token) when the kernel's occupancy lets the device hold
+ * the grid, else cooperative anyway; the CALLER guarantees that no other
+ * kernel (another stream, another process, a fill on a side stream) holds
+ * CUs of the device while it runs.  The kernel's waits are bounded: an
+ * ordinary launch whose grid could not be placed at once ends with
+ * MOE_ERR_TIMEOUT from moe_check_device_error, never a hang; rerun that
+ * token cooperatively on a zeroed workspace (epoch 1).
  * This fuses the per-layer calls of streaming_call (engine_v3.py:493-609) for
  * a device-resident pool; it has no single counterpart in the reference.
  */
@@ -220,8 +236,8 @@ int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_lay
                      const uint16_t *bias, int32_t mode, int32_t renorm, int32_t k_pred,
                      const int32_t *table, uint16_t *y, int32_t *ids, float *scores,
                      int32_t *slot_refs, int32_t *pred, int32_t *miss_count,
-                     uint32_t epoch, void *workspace, size_t workspace_bytes,
-                     void *stream);
+                     uint32_t epoch, int32_t flags, void *workspace,
+                     size_t workspace_bytes, void *stream);
 
 /*
  * Device-side (layer, expert) -> slot lookup for n ids (the index build of
@@ -235,14 +251,17 @@ int moe_slot_lookup(const int32_t *table, int32_t E, const int32_t *ids,
 
 /* Slot fills: copy n whole expert records into pool slots.
  * src_records: record indices into `src_store` (host pinned or device
- * memory laid out like pool->store; NULL means pool->store), dst_slots: pool
- * slots.  Host index arrays.  Enqueued on `stream`: a source the GPU can
+ * memory laid out like pool->store, src_n_records records of
+ * src_record_bytes; NULL means pool->store with the view's record size and
+ * count), dst_slots: pool slots.  Host index arrays; every index is range
+ * checked on the host (MOE_ERR_INVALID) before anything is enqueued.  Enqueued on `stream`: a source the GPU can
  * read (HBM or pinned host memory) is copied by kernels, up to 160 records
  * per launch; pageable memory by hipMemcpyAsync per component.  Replaces
  * ExpertPool._read (engine_v3.py:255-290). */
 int moe_fill_slots(const moe_pool_view *pool, const void *src_store,
-                   int64_t src_record_bytes, const int64_t *src_records,
-                   const int32_t *dst_slots, int32_t n, void *stream);
+                   int64_t src_record_bytes, int64_t src_n_records,
+                   const int64_t *src_records, const int32_t *dst_slots, int32_t n,
+                   void *stream);
 
 /* Pinned host memory for the expert store (hipHostMalloc). */
 int moe_host_alloc(size_t bytes, void **out);
@@ -257,8 +276,10 @@ int moe_event_query(void *ev);                 /* 1 done, 0 pending, <0 err */
 int moe_stream_wait_event(void *stream, void *ev);
 int moe_event_elapsed_ms(void *start, void *stop, float *ms);
 
-/* Read and clear the device error word set by the kernels (out-of-range slot
- * refs), synchronising `stream`.  Returns MOE_OK or MOE_ERR_DEVICE. */
+/* Read and clear the device error word set by the kernels, synchronising
+ * `stream`.  Returns MOE_OK, MOE_ERR_TIMEOUT (a bounded cross-workgroup wait
+ * gave up; the message also says if a slot ref was out of range) or
+ * MOE_ERR_DEVICE (an out-of-range slot ref, whose contribution was zero). */
 int moe_check_device_error(void *stream);
 
 /*

@@ -19,6 +19,10 @@ MOE_ERR_UNSUPPORTED = -2
 MOE_ERR_HIP = -3
 MOE_ERR_EXHAUSTED = -4
 MOE_ERR_DEVICE = -5
+MOE_ERR_TIMEOUT = -6
+
+MOE_STACK_COOPERATIVE = 0
+MOE_STACK_ORDINARY = 1
 
 MOE_ACT_SWIGLU = 0
 MOE_ACT_SWIGLU_CLAMP = 1
@@ -99,8 +103,8 @@ def _declare(lib):
         "moe_stack_trace": (C.c_int, [P, SZ]),
         "moe_stack_decode": (C.c_int, [C.POINTER(PoolView), C.POINTER(Geom), I32, I32, I32,
                                        P, P, P, I32, I32, I32, P, P, P, P, P, P, P,
-                                       C.c_uint32, P, SZ, P]),
-        "moe_fill_slots": (C.c_int, [C.POINTER(PoolView), P, I64, P, P, I32, P]),
+                                       C.c_uint32, I32, P, SZ, P]),
+        "moe_fill_slots": (C.c_int, [C.POINTER(PoolView), P, I64, I64, P, P, I32, P]),
         "moe_host_alloc": (C.c_int, [SZ, C.POINTER(C.c_void_p)]),
         "moe_host_free": (C.c_int, [P]),
         "moe_event_create": (C.c_int, [C.POINTER(C.c_void_p)]),

@@ -374,12 +374,13 @@ int moe_stack_trace(void *device_buf, size_t bytes) {
 
 size_t moe_stack_workspace(const moe_geom *g, int32_t n_layers, int32_t E, int32_t k) {
   if (!g || n_layers <= 0 || E <= 0 || k <= 0) return 0;
+  const size_t abort_w = 256;   // the launch's abort word, on a line of its own
   const size_t counters = (size_t)n_layers * moe::kCountersPerLayer * moe::kCounterWords * 4;
   const size_t logits = ((size_t)2 * E * 8 + 255) & ~(size_t)255;   // flagged entries
   // flagged activations (2 bf16 + flag per 8 bytes): predicted (+ spares), fix-up
   const size_t hp = ((size_t)(k + moe::kSpare) * (g->d_ff / 2) * 8 + 255) & ~(size_t)255;
   const size_t hf = ((size_t)k * (g->d_ff / 2) * 8 + 255) & ~(size_t)255;
-  return counters + logits + hp + hf;
+  return abort_w + counters + logits + hp + hf;
 }
 
 int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_layers,
@@ -387,8 +388,8 @@ int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_lay
                      const uint16_t *bias, int32_t mode, int32_t renorm, int32_t k_pred,
                      const int32_t *table, uint16_t *y, int32_t *ids, float *scores,
                      int32_t *slot_refs, int32_t *pred, int32_t *miss_count,
-                     uint32_t epoch, void *workspace, size_t workspace_bytes,
-                     void *stream) {
+                     uint32_t epoch, int32_t flags, void *workspace,
+                     size_t workspace_bytes, void *stream) {
   moe::PoolArgs pa;
   int rc = make_pool_args(pool, g, &pa);
   if (rc) return rc;
@@ -416,6 +417,7 @@ int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_lay
   if (workspace_bytes < moe_stack_workspace(g, n_layers, E, k))
     return fail(MOE_ERR_INVALID, "workspace %zu < %zu bytes", workspace_bytes,
                 moe_stack_workspace(g, n_layers, E, k));
+  if (flags & ~MOE_STACK_ORDINARY) return fail(MOE_ERR_INVALID, "unknown flags 0x%x", flags);
   if (epoch == 0) return fail(MOE_ERR_INVALID, "epoch must start at 1");
   if ((uint64_t)epoch * (uint64_t)n_layers + (uint64_t)n_layers > 0xffffffffull)
     return fail(MOE_ERR_INVALID, "epoch %u too large for %d layers: zero the workspace and "
@@ -433,6 +435,8 @@ int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_lay
   a.refs_out = slot_refs;
   a.pred = pred;
   a.miss = miss_count;
+  a.abort_w = reinterpret_cast<uint32_t *>(ws);
+  ws += 256;
   a.cnt = reinterpret_cast<uint32_t *>(ws);
   ws += (size_t)n_layers * moe::kCountersPerLayer * moe::kCounterWords * 4;
   a.lgt = reinterpret_cast<uint64_t *>(ws);
@@ -457,7 +461,8 @@ int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_lay
     a.trace = g_stack_trace;
   }
   (void)hipGetLastError();
-  MOE_HIP(moe::launch_stack(S, a, static_cast<hipStream_t>(stream)));
+  MOE_HIP(moe::launch_stack(S, a, (flags & MOE_STACK_ORDINARY) != 0,
+                            static_cast<hipStream_t>(stream)));
   return MOE_OK;
 }
 
@@ -553,15 +558,18 @@ const char *kernel_address(const void *p, bool *host) {
 }  // namespace
 
 int moe_fill_slots(const moe_pool_view *pool, const void *src_store,
-                   int64_t src_record_bytes, const int64_t *src_records,
-                   const int32_t *dst_slots, int32_t n, void *stream) {
+                   int64_t src_record_bytes, int64_t src_n_records,
+                   const int64_t *src_records, const int32_t *dst_slots, int32_t n,
+                   void *stream) {
   if (!pool) return fail(MOE_ERR_INVALID, "pool view is NULL");
   if (n < 0) return fail(MOE_ERR_INVALID, "n < 0");
   if (n == 0) return MOE_OK;
   if (!src_records || !dst_slots) return fail(MOE_ERR_INVALID, "NULL index arrays");
   const char *src = static_cast<const char *>(src_store ? src_store : pool->store);
   const int64_t rb = src_store ? src_record_bytes : pool->record_bytes;
+  const int64_t nrec = src_store ? src_n_records : pool->n_records;
   if (!src || rb <= 0) return fail(MOE_ERR_INVALID, "no source store");
+  if (nrec <= 0) return fail(MOE_ERR_INVALID, "source store of %lld records", (long long)nrec);
   const int nc = pool->n_components;
   if (nc != 9 && nc != 12) return fail(MOE_ERR_INVALID, "n_components=%d", nc);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -570,8 +578,9 @@ int moe_fill_slots(const moe_pool_view *pool, const void *src_store,
     const int64_t rec = src_records[i];
     if (slot < 0 || slot >= pool->n_slots)
       return fail(MOE_ERR_INVALID, "slot %d outside [0, %d)", slot, pool->n_slots);
-    if (rec < 0 || (!src_store && rec >= pool->n_records))
-      return fail(MOE_ERR_INVALID, "record %lld out of range", (long long)rec);
+    if (rec < 0 || rec >= nrec)
+      return fail(MOE_ERR_INVALID, "record %lld outside [0, %lld)", (long long)rec,
+                  (long long)nrec);
   }
   // Copy kernels for a source the GPU can read (HBM, or pinned host memory
   // over the link: one launch per batch instead of a copy call per
@@ -692,6 +701,12 @@ int moe_check_device_error(void *stream) {
     const int zero = 0;
     MOE_HIP(hipMemcpyToSymbol(HIP_SYMBOL(moe::g_device_error), &zero, sizeof(int), 0,
                               hipMemcpyHostToDevice));
+    if (v & moe::kErrTimeout)
+      return fail(MOE_ERR_TIMEOUT,
+                  "a kernel's wait for another workgroup gave up (its grid was not resident "
+                  "at once: another kernel held CUs of the device)%s",
+                  (v & moe::kErrBadRef) ? "; a kernel also resolved an out-of-range slot "
+                                          "reference" : "");
     return fail(MOE_ERR_DEVICE, "a kernel resolved an out-of-range slot reference");
   }
   return MOE_OK;

@@ -240,10 +240,17 @@ __device__ __forceinline__ const char *resolve_packed_safe(const PoolArgs &pa, i
   return ok ? p : (pa.n_slots > 0 ? pa.base[c] : pa.store + L::comp_offset(c));
 }
 
-__device__ __forceinline__ void flag_error() {
-  __hip_atomic_store(&g_device_error, 1, __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
+// Bits of the device error word.
+constexpr int kErrBadRef = 1;    // a slot reference outside the pool view
+constexpr int kErrTimeout = 2;   // a bounded cross-workgroup wait gave up
+
+__device__ __forceinline__ void flag_error_bits(int bits) {
+  __hip_atomic_fetch_or(&g_device_error, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// an out-of-range slot reference (the kernel contributes zeros for it)
+__device__ __forceinline__ void flag_error() { flag_error_bits(kErrBadRef); }
+// a bounded wait for another workgroup ran past its spin limit
+__device__ __forceinline__ void flag_timeout() { flag_error_bits(kErrTimeout); }
 
 // Component indices inside a pool view.
 __host__ __device__ constexpr int comp_index(int proj, int part, int nparts) {

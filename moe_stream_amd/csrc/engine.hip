@@ -144,7 +144,8 @@ int engine_fill(moe_engine *e, int32_t layer, const int32_t *experts, const int3
   if (n <= 0) return MOE_OK;
   std::vector<int64_t> recs(n);
   for (int32_t i = 0; i < n; ++i) recs[i] = (int64_t)layer * e->E + experts[i];
-  const int rc = moe_fill_slots(&e->pool, e->store, e->record_bytes, recs.data(), slots, n, s);
+  const int rc =
+      moe_fill_slots(&e->pool, e->store, e->record_bytes, e->n_records, recs.data(), slots, n, s);
   if (rc) return rc;
   e->bytes_read += (int64_t)n * e->record_bytes;
   return MOE_OK;

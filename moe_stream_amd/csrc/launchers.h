@@ -83,7 +83,7 @@ struct StackLaunch {
   const void *func;
 };
 const StackLaunch *find_stack(int d_model, int d_ff, int k, int has_bias);
-hipError_t launch_stack(const StackLaunch *S, StackArgs &a, hipStream_t s);
+hipError_t launch_stack(const StackLaunch *S, StackArgs &a, bool ordinary, hipStream_t s);
 void launch_slot_lookup(const int32_t *table, int E, const int32_t *ids, int n,
                         int32_t *refs, int32_t *miss_count, hipStream_t s);
 

@@ -205,7 +205,7 @@ __device__ __forceinline__ void poll_logits(const uint64_t *lg, int E, uint32_t 
     const bool ok = (uint32_t)(v0 >> 32) == fl && (uint32_t)(v1 >> 32) == fl;
     if (__all(ok)) return;
     if (spins > kRouteSpinLimit) {
-      if (lane == 0) flag_error();
+      if (lane == 0) flag_timeout();
       return;
     }
     __builtin_amdgcn_s_sleep(1);

@@ -63,7 +63,8 @@ struct StackArgs {
   uint64_t *lgt;          // ws [2][E] router / lookahead logits, flagged (put_logit)
   uint64_t *hpred;        // ws [K + kSpare][F/2] activations of the predicted experts and
   uint64_t *hfix;         // ws [K][F/2] of the fix-up slots: 2 bf16 + layer flag each
-  uint32_t *cnt;          // ws [L][3][kSub] counters, 128 B apart
+  uint32_t *cnt;          // ws [L][kSub] counters, 128 B apart
+  uint32_t *abort_w;      // ws: epoch of the launch in which a wait gave up
   int L, E, kp, mode, renorm, act;
   float alpha, limit;
   uint32_t epoch;
@@ -128,30 +129,45 @@ __device__ __forceinline__ uint32_t *counter(const StackArgs &a, int l, int whic
   return a.cnt + ((size_t)l * kCountersPerLayer + which) * kCounterWords;
 }
 
-// The device error word, loaded in the same batch as a poll's loads, so a
-// poll that misses costs one round trip, not a second one for this check.
-__device__ __forceinline__ int poll_error_word() {
-  return __hip_atomic_load(&g_device_error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// The launch's abort word (in the workspace): the epoch of the launch in
+// which some wait gave up.  Every poll loads it in the same batch as its own
+// loads (a poll that misses costs one round trip, not a second one for this
+// check), so once one wait has timed out the others stop at their next miss
+// instead of each running to the spin limit.  A value left by an earlier
+// launch never equals the current epoch, so it cannot cut a new launch short.
+struct Abort {
+  uint32_t *word;
+  uint32_t ep;
+  __device__ __forceinline__ uint32_t load() const {
+    return __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // one lane: this launch gives up (and the device error word says why)
+  __device__ __forceinline__ void raise() const {
+    __hip_atomic_store(word, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    flag_timeout();
+  }
+};
 
 // One whole wave: poll until the counter's sum >= target (no barrier).
 // Bounded: past the spin limit, or as soon as any workgroup has flagged an
 // error, it gives up (wrong results, never a hang).
-__device__ __forceinline__ void wave_wait(const uint32_t *c, uint32_t target) {
+__device__ __forceinline__ void wave_wait(const uint32_t *c, uint32_t target, const Abort &ab) {
   const int lane = threadIdx.x & 63;
   uint32_t spins = 0;
   while (true) {
     int v = (lane < kSub) ? (int)__hip_atomic_load(c + lane * 32, __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT)
                           : 0;
-    const int err = poll_error_word();
+    const uint32_t abw = ab.load();
     v += dpp_i<kDppQuadXor1>(v);
     v += dpp_i<kDppQuadXor2>(v);
     v += dpp_i<kDppHalfMirror>(v);
     const uint32_t sum = (uint32_t)__builtin_amdgcn_readfirstlane(v);
-    if (sum >= target) break;
-    if (++spins > kSpinLimit || __builtin_amdgcn_readfirstlane(err)) {
-      if (lane == 0) flag_error();
+    // counters are monotonic modulo 2^32: compare the distance, not the values
+    if ((int32_t)(sum - target) >= 0) break;
+    if (__builtin_amdgcn_readfirstlane(abw) == ab.ep) break;   // another wait gave up
+    if (++spins > kSpinLimit) {
+      if (lane == 0) ab.raise();
       break;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -161,21 +177,22 @@ __device__ __forceinline__ void wave_wait(const uint32_t *c, uint32_t target) {
 // One whole wave: the logits of entries lane and lane + 64 of `slots` (n
 // entries, n <= 128), polled until every present entry carries `fl`.
 // Bounded like wave_wait.
-__device__ __forceinline__ void get_logits(const uint64_t *slots, int n, uint32_t fl, float &z0,
-                                           float &z1) {
+__device__ __forceinline__ void get_logits(const uint64_t *slots, int n, uint32_t fl,
+                                           const Abort &ab, float &z0, float &z1) {
   const int lane = threadIdx.x & 63, e0 = lane, e1 = lane + 64;
   const uint64_t *p0 = slots + min(e0, n - 1), *p1 = slots + min(e1, n - 1);
   uint32_t spins = 0;
   while (true) {
     const uint64_t v0 = __hip_atomic_load(p0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint64_t v1 = __hip_atomic_load(p1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int err = poll_error_word();
+    const uint32_t abw = ab.load();
     const bool ok = (e0 >= n || (uint32_t)(v0 >> 32) == fl) && (e1 >= n || (uint32_t)(v1 >> 32) == fl);
     z0 = __uint_as_float((uint32_t)v0);
     z1 = __uint_as_float((uint32_t)v1);
     if (__ballot(!ok) == 0) break;
-    if (++spins > kSpinLimit || __builtin_amdgcn_readfirstlane(err)) {
-      if (lane == 0) flag_error();
+    if (__builtin_amdgcn_readfirstlane(abw) == ab.ep) break;   // another wait gave up
+    if (++spins > kSpinLimit) {
+      if (lane == 0) ab.raise();
       break;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -186,8 +203,9 @@ __device__ __forceinline__ void get_logits(const uint64_t *slots, int n, uint32_
 // Wave `poll_wave` polls the sub-counters (device scope); the barrier then
 // releases the workgroup, whose later device-scope loads observe every store
 // that was complete before the arrivals counted.
-__device__ __forceinline__ void wg_wait(const uint32_t *c, uint32_t target, int poll_wave) {
-  if ((threadIdx.x >> 6) == poll_wave) wave_wait(c, target);
+__device__ __forceinline__ void wg_wait(const uint32_t *c, uint32_t target, int poll_wave,
+                                        const Abort &ab) {
+  if ((threadIdx.x >> 6) == poll_wave) wave_wait(c, target, ab);
   __syncthreads();
 }
 
@@ -494,7 +512,8 @@ __device__ __forceinline__ void fix_task(const StackArgs &a, int32_t ref, int b,
 // per lane (pieces lane and lane + 64, 8 bf16 each), polled until every entry
 // carries the flag `fl`.  Bounded like wave_wait.
 template <int HU4>
-__device__ __forceinline__ void get_acts(const uint64_t *hf, uint32_t fl, uint4 &p0, uint4 &p1) {
+__device__ __forceinline__ void get_acts(const uint64_t *hf, uint32_t fl, const Abort &ab,
+                                         uint4 &p0, uint4 &p1) {
   const int lane = threadIdx.x & 63;
   const uint64_t *e0 = hf + 4 * min(lane, HU4 - 1), *e1 = hf + 4 * min(lane + 64, HU4 - 1);
   uint32_t spins = 0;
@@ -505,15 +524,16 @@ __device__ __forceinline__ void get_acts(const uint64_t *hf, uint32_t fl, uint4 
       v[q] = __hip_atomic_load(e0 + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       v[4 + q] = __hip_atomic_load(e1 + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    const int err = poll_error_word();
+    const uint32_t abw = ab.load();
     bool ok = true;
 #pragma unroll
     for (int q = 0; q < 8; ++q) ok = ok && (uint32_t)(v[q] >> 32) == fl;
     p0 = make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
     p1 = make_uint4((uint32_t)v[4], (uint32_t)v[5], (uint32_t)v[6], (uint32_t)v[7]);
     if (__ballot(!ok) == 0) break;
-    if (++spins > kSpinLimit || __builtin_amdgcn_readfirstlane(err)) {
-      if (lane == 0) flag_error();
+    if (__builtin_amdgcn_readfirstlane(abw) == ab.ep) break;   // another wait gave up
+    if (++spins > kSpinLimit) {
+      if (lane == 0) ab.raise();
       break;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -629,6 +649,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wg = blockIdx.x;
   const uint32_t ep = a.epoch;
+  const Abort ab{a.abort_w, ep};
   const int upos = wg / NPOS, urow0 = (wg % NPOS) * ROWS_U;   // gate/up block
   const int drow0 = wg * ROWS_D;                               // down block
   const int dj = lane % SGD, dsub = lane / SGD;
@@ -673,7 +694,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
     // flight here (loads complete in order, so a poll issued behind staging
     // loads would return only after them); it issues its own down staging
     // right after
-    if (l > 0) wg_wait(counter(a, l - 1, CNT_D), ep * C::ITEMS_D, W_RANK);
+    if (l > 0) wg_wait(counter(a, l - 1, CNT_D), ep * C::ITEMS_D, W_RANK, ab);
     else __syncthreads();
     if (wave == 0) trace_mark(a, l, TR_R_WAITED);
     const int pcnt = pred_cnt[l & 1];
@@ -763,7 +784,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
         const int32_t *tabn = a.table + (size_t)(l + 1) * a.E;
         const int32_t t0 = tabn[min(e0, a.E - 1)], t1 = tabn[min(e1, a.E - 1)];
         float l0, l1;
-        get_logits(a.lgt + a.E, a.E, layer_flag(a, l), l0, l1);
+        get_logits(a.lgt + a.E, a.E, layer_flag(a, l), ab, l0, l1);
         const float z0 = e0 < a.E ? round_bf16(l0 + b0) : -INFINITY;
         const float z1 = e1 < a.E ? round_bf16(l1 + b1) : -INFINITY;
         bool s0, s1;
@@ -801,7 +822,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       // every expert's slot ref, also before the wait (clamped, unconditional)
       const int32_t t0 = tab[min(e0, a.E - 1)], t1 = tab[min(e1, a.E - 1)];
       float l0, l1;
-      get_logits(a.lgt, a.E, layer_flag(a, l), l0, l1);
+      get_logits(a.lgt, a.E, layer_flag(a, l), ab, l0, l1);
       trace_mark(a, l, TR_R_ALL);
       const float z0 = e0 < a.E ? round_bf16(l0 + b0) : -INFINITY;
       const float z1 = e1 < a.E ? round_bf16(l1 + b1) : -INFINITY;
@@ -953,7 +974,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
         const uint64_t *hf = fx < 0    ? a.hpred + (size_t)wave * (F / 2)
                              : src >= 0 ? a.hfix + (size_t)src * (F / 2)
                                         : a.hpred + (size_t)(K - 1 - src) * (F / 2);
-        get_acts<HU4>(hf, layer_flag(a, l), p0, p1);
+        get_acts<HU4>(hf, layer_flag(a, l), ab, p0, p1);
         if (wave == 0) trace_mark(a, l, TR_D_WAITED);
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
@@ -1033,32 +1054,35 @@ const StackLaunch *find_stack(int d_model, int d_ff, int k, int has_bias) {
 }
 
 // Every workgroup of the kernel waits for every other, so the whole grid
-// must be resident at once.  When the kernel's occupancy lets one device
-// hold the grid (one workgroup per CU; checked once per device and kernel),
-// an ordinary launch places every workgroup on a device not shared with
-// other kernels, and its dispatch costs ~16 us less per token than a
-// cooperative launch's; the kernel's waits are bounded, so a concurrent
-// kernel holding CUs past them makes it report a device error rather than
-// wait.  Where the check fails, the cooperative launch gives the guarantee.
-hipError_t launch_stack(const StackLaunch *S, StackArgs &a, hipStream_t s) {
+// must be resident at once.  The cooperative launch guarantees that.  An
+// ordinary launch (the caller's choice, `ordinary`) costs ~16 us less per
+// token to dispatch and places every workgroup only while no other kernel
+// holds CUs of the device: it is taken when the kernel's occupancy lets one
+// device hold the grid (checked once per device and kernel), else the launch
+// is cooperative anyway.  The kernel's waits are bounded, so an ordinary
+// launch that could not place its whole grid ends with the timeout bit in
+// the device error word, never a hang.
+hipError_t launch_stack(const StackLaunch *S, StackArgs &a, bool ordinary, hipStream_t s) {
   void *args[] = {&a};
-  constexpr int kMaxDevices = 64;
-  static std::atomic<int> fits[kMaxDevices][kStackKernels];   // 0 unknown, 1 yes, 2 no
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return e;
-  const int ki = (int)(S - kStackTable);
-  int f = (dev >= 0 && dev < kMaxDevices) ? fits[dev][ki].load() : 2;
-  if (f == 0) {
-    int per_cu = 0, cus = 0;
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, S->func, 512, 0);
-    if (e == hipSuccess)
-      e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (ordinary) {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> fits[kMaxDevices][kStackKernels];   // 0 unknown, 1 yes, 2 no
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    f = (int64_t)per_cu * cus >= S->nwg ? 1 : 2;
-    fits[dev][ki].store(f);
+    const int ki = (int)(S - kStackTable);
+    int f = (dev >= 0 && dev < kMaxDevices) ? fits[dev][ki].load() : 2;
+    if (f == 0) {
+      int per_cu = 0, cus = 0;
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, S->func, 512, 0);
+      if (e == hipSuccess)
+        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+      if (e != hipSuccess) return e;
+      f = (int64_t)per_cu * cus >= S->nwg ? 1 : 2;
+      fits[dev][ki].store(f);
+    }
+    if (f == 1) return hipLaunchKernel(S->func, dim3(S->nwg), dim3(512), args, 0, s);
   }
-  if (f == 1) return hipLaunchKernel(S->func, dim3(S->nwg), dim3(512), args, 0, s);
   return hipLaunchCooperativeKernel(S->func, dim3(S->nwg), dim3(512), args, 0, s);
 }
 

@@ -23,6 +23,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import time
 
 import numpy as np
 import torch
@@ -124,7 +125,7 @@ class SlotPool:
         if len(sl) and (sl.min() < 0 or sl.max() >= self.n_slots):
             raise ValueError(f"slot outside [0, {self.n_slots})")
         _lib.check(_lib.lib().moe_fill_slots(
-            C.byref(self.c_view()), sp, rb, recs.ctypes.data, sl.ctypes.data,
+            C.byref(self.c_view()), sp, rb, nr, recs.ctypes.data, sl.ctypes.data,
             len(sl), _lib.stream_ptr(stream)))
 
     def read_slot(self, slot: int) -> dict:
@@ -132,17 +133,41 @@ class SlotPool:
         return {n: a[slot].cpu() for n, a in self.views.items()}
 
 
+# The reference's defaults (engine_v3.py:59-60): pool slots and fill workers.
+N_SLOTS = int(os.environ.get("PF_SLOTS", "3072"))
+N_WORKERS = int(os.environ.get("PF_WORKERS", "4"))
+
+
 class ExpertPool(SlotPool):
     """Fixed pool of expert slots with stream-ordered fills and LFU eviction;
     the API of engine_v3.ExpertPool (engine_v3.py:125-464): `prefetch`,
     `acquire`, `stats`, `views`, `slot_of`, `pending`, `pinned`,
-    `needs_barrier`, `bytes_read`, `_read`."""
+    `needs_barrier`, `bytes_read`, `_read`.
 
-    def __init__(self, geom: Geometry, n_slots: int, store, device="cuda",
-                 evict: str | None = None, depths=(1,), widen: int = 1,
-                 side_stream: torch.cuda.Stream | None = None,
+    Construction as the reference's, ExpertPool(model_dir, n_slots,
+    n_workers) (engine_v3.py:128): `model_dir` holds experts.bin +
+    experts_index.json, whose records are loaded into a pinned host store by
+    `n_workers` reader threads; fills then cross the host link from there.
+    Or ExpertPool(geom, n_slots, store=...) over a store already in pinned
+    host memory (HostStore) or HBM (uint8 [n_records, record_bytes])."""
+
+    def __init__(self, model_dir, n_slots: int = N_SLOTS, n_workers: int = N_WORKERS,
+                 store=None, device="cuda", evict: str | None = None, depths=(1,),
+                 widen: int = 1, side_stream: torch.cuda.Stream | None = None,
                  n_layers: int | None = None):
+        if isinstance(model_dir, Geometry):
+            geom = model_dir
+            if store is None:
+                raise ValueError("ExpertPool(geom, ...) needs store=")
+        else:
+            from .store import ExpertStoreFile
+            sf = ExpertStoreFile(os.fspath(model_dir))
+            geom = sf.geom
+            if store is None:
+                store = sf.to_host_store(n_workers=n_workers)
+            n_layers = n_layers or sf.index.n_layers
         super().__init__(geom, n_slots, device, store)
+        self.n_workers = n_workers
         self.n_experts = geom.n_experts
         self.n_layers = n_layers or geom.n_layers
         self.top_k = geom.top_k
@@ -163,9 +188,62 @@ class ExpertPool(SlotPool):
         self.bytes_read = 0
         self.bytes_exposed = 0
         self.side = side_stream if side_stream is not None else torch.cuda.Stream(device=self.device)
+        # telemetry of engine_v3.py:238-250, for stream-ordered fills:
+        # t_blocked = host seconds inside acquire from issuing its misses to
+        # returning; busy_s = device seconds with >= 1 fill in flight (from
+        # timing events around every fill batch); depth = mean number of
+        # records in flight when a record's fill is issued
+        self.t_blocked = 0.0
+        self.depth_sum = 0
+        self.depth_n = 0
+        self._fills = []             # (start event, end event, records) in flight
+        self._spans = []             # completed fills: (start ms, end ms) from _t0
+        self._busy_done_ms = 0.0     # busy time of spans already merged away
+        self._t0 = torch.cuda.Event(enable_timing=True)
+        self._t0.record(torch.cuda.current_stream(self.device))
 
     def _record(self, layer, expert) -> int:
         return layer * self.n_experts + int(expert)
+
+    def _retire_fills(self):
+        keep = []
+        for a, b, n in self._fills:
+            if b.query():
+                self._spans.append((self._t0.elapsed_time(a), self._t0.elapsed_time(b)))
+            else:
+                keep.append((a, b, n))
+        self._fills = keep
+        if len(self._spans) > 4096:
+            self._merge_spans(keep_last=True)
+
+    def _merge_spans(self, keep_last: bool):
+        """Fold completed spans into busy time (a union of intervals); with
+        keep_last the latest merged interval stays open for later overlaps."""
+        spans = sorted(self._spans)
+        merged = []
+        for a, b in spans:
+            if merged and a <= merged[-1][1]:
+                merged[-1][1] = max(merged[-1][1], b)
+            else:
+                merged.append([a, b])
+        last = merged.pop() if (keep_last and merged) else None
+        self._busy_done_ms += sum(b - a for a, b in merged)
+        self._spans = [tuple(last)] if last is not None else []
+
+    def _fill_tracked(self, records, slots, stream):
+        """fill() with the telemetry of _read (engine_v3.py:255-262, 286-290)."""
+        self._retire_fills()
+        inflight = sum(n for _, _, n in self._fills)
+        n = len(slots)
+        self.depth_sum += n * inflight + n * (n + 1) // 2
+        self.depth_n += n
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        self.fill(records, slots, stream=stream)
+        b.record(stream)
+        self._fills.append((a, b, n))
+        self.bytes_read += n * self.blob
 
     def poll(self):
         """Retire prefetch fills whose events have completed
@@ -177,8 +255,8 @@ class ExpertPool(SlotPool):
 
     def _read(self, slot, layer, expert, stream=None):
         """Fill one slot now, on `stream` (default: the current stream)."""
-        self.fill([self._record(layer, expert)], [slot], stream=stream)
-        self.bytes_read += self.blob
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        self._fill_tracked([self._record(layer, expert)], [slot], s)
 
     # -- public (engine_v3.py:383-464) --------------------------------------
     def prefetch(self, layer, experts):
@@ -189,12 +267,11 @@ class ExpertPool(SlotPool):
         if len(slots):
             compute = torch.cuda.current_stream(self.device)
             self.side.wait_stream(compute)          # no refill under a running kernel
-            self.fill([self._record(layer, e) for e in exps], slots, stream=self.side)
+            self._fill_tracked([self._record(layer, e) for e in exps], slots, self.side)
             ev = torch.cuda.Event()
             ev.record(self.side)
             for e in exps:
                 self.pending[(layer, int(e))] = ev
-            self.bytes_read += len(slots) * self.blob
 
     def acquire(self, layer, experts):
         """The slot holding each expert.  Misses are filled on the compute
@@ -206,15 +283,16 @@ class ExpertPool(SlotPool):
             slots, miss, wait = self.policy.acquire(layer, experts)
         except PoolExhausted as e:
             raise RuntimeError(str(e)) from None
+        t0 = time.perf_counter()
         ex = np.asarray(experts).reshape(-1)
         if len(miss):
-            self.fill([self._record(layer, ex[i]) for i in miss], slots[miss], stream=compute)
-            self.bytes_read += len(miss) * self.blob
+            self._fill_tracked([self._record(layer, ex[i]) for i in miss], slots[miss], compute)
             self.bytes_exposed += len(miss) * self.blob
         for i in wait:
             ev = self.pending.pop((layer, int(ex[i])), None)
             if ev is not None:
                 compute.wait_event(ev)
+        self.t_blocked += time.perf_counter() - t0
         self.pinned = set(int(s) for s in slots)
         return [int(s) for s in slots]
 
@@ -222,8 +300,18 @@ class ExpertPool(SlotPool):
         """int32 [n_layers, n_experts] slot table on the device (-1 = absent)."""
         return torch.from_numpy(self.policy.table()).to(self.device)
 
+    def busy_s(self) -> float:
+        """Device seconds with at least one fill in flight (fills completed
+        so far)."""
+        self._retire_fills()
+        self._merge_spans(keep_last=True)
+        return (self._busy_done_ms + sum(b - a for a, b in self._spans)) / 1e3
+
     def stats(self):
+        """The reference's keys (engine_v3.py:456-464)."""
         s = self.policy.stats()
         return dict(total=s["total"], prefetch=s["prefetch"], cache=s["cache"],
-                    miss=s["miss"], gb=self.bytes_read / 2 ** 30, bail=s["bail"],
-                    issued=s["issued"], exposed_gb=self.bytes_exposed / 2 ** 30)
+                    miss=s["miss"], blocked=self.t_blocked, gb=self.bytes_read / 2 ** 30,
+                    busy_s=self.busy_s(), depth=self.depth_sum / max(1, self.depth_n),
+                    bail=s["bail"], issued=s["issued"],
+                    exposed_gb=self.bytes_exposed / 2 ** 30)

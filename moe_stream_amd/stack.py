@@ -140,6 +140,15 @@ class DecodeStack:
             (self.geom.d_model, self.geom.d_ff, self.k, self.geom.has_proj_bias) in \
             {(2048, 768, 8, False)}
 
+    # the launch count after which the persistent workspace is zeroed and the
+    # epoch restarts at 1 (the kernel's per-layer flags, epoch * n_layers + l,
+    # must stay below 2^32)
+    EPOCH_RESTART = 1 << 22
+
+    @staticmethod
+    def epoch_limit(n_layers: int) -> int:
+        return min(DecodeStack.EPOCH_RESTART, (2 ** 32 - 1) // n_layers - 2)
+
     def _persistent_buffers(self):
         import ctypes as C
         g = self.geom.c_geom()
@@ -154,24 +163,70 @@ class DecodeStack:
         self.p_miss = torch.zeros((self.L,), dtype=torch.int32, device=dev)
         self.p_y = torch.zeros((self.L, self.geom.d_model), dtype=torch.bfloat16, device=dev)
 
-    def token_persistent(self, x_tok: torch.Tensor, stream=None):
-        """All layers of one token in one cooperative launch.  x_tok: bf16
-        [n_layers, d_model]; outputs in p_y, p_ids, p_scores, p_refs, p_pred,
-        p_miss."""
+    def reset_persistent(self, stream=None):
+        """Zero the persistent kernel's workspace (on `stream`) and restart
+        its epoch at 1: required after a failed launch and before the epoch
+        bound."""
+        if not hasattr(self, "p_ws"):
+            self._persistent_buffers()
+            return
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        with torch.cuda.stream(s):
+            self.p_ws.zero_()
+        self.p_epoch = 0
+
+    def token_persistent(self, x_tok: torch.Tensor, stream=None, ordinary: bool = False):
+        """All layers of one token in one launch.  x_tok: bf16 [n_layers,
+        d_model]; outputs in p_y, p_ids, p_scores, p_refs, p_pred, p_miss.
+
+        ordinary=False: a cooperative launch.  ordinary=True: an ordinary
+        launch, for a caller that guarantees no other kernel runs on the
+        device meanwhile; if that guarantee fails, check_persistent() reports
+        MOE_ERR_TIMEOUT and the tokens must be run again."""
         import ctypes as C
         if not hasattr(self, "p_ws"):
             self._persistent_buffers()
+        if self.p_epoch >= self.epoch_limit(self.L):
+            self.reset_persistent(stream)
         x_tok = x_tok.contiguous()
         self.p_epoch += 1
         g = self.geom.c_geom()
         b = self.bias.data_ptr() if self.bias is not None else None
+        flags = _lib.MOE_STACK_ORDINARY if ordinary else _lib.MOE_STACK_COOPERATIVE
         _lib.check(_lib.lib().moe_stack_decode(
             C.byref(self.pool.c_view()), C.byref(g), self.L, self.E, self.k,
             x_tok.data_ptr(), self.W.data_ptr(), b, self.geom.routing,
             int(self.geom.norm_topk_prob), self.k_pred, self.table.data_ptr(),
             self.p_y.data_ptr(), self.p_ids.data_ptr(), self.p_scores.data_ptr(),
             self.p_refs.data_ptr(), self.p_pred.data_ptr(), self.p_miss.data_ptr(),
-            self.p_epoch, self.p_ws.data_ptr(), self.p_ws.numel(), _lib.stream_ptr(stream)))
+            self.p_epoch, flags, self.p_ws.data_ptr(), self.p_ws.numel(),
+            _lib.stream_ptr(stream)))
+
+    def check_persistent(self, stream=None):
+        """Synchronise `stream` and read the device error word.  On an error
+        the workspace is reset (the next launch starts at epoch 1) and the
+        error is raised: MoeError with code MOE_ERR_TIMEOUT when a launch's
+        grid was not resident at once (run those tokens again, cooperatively),
+        MOE_ERR_DEVICE for an out-of-range slot reference."""
+        rc = _lib.lib().moe_check_device_error(_lib.stream_ptr(stream))
+        if rc < 0:
+            self.reset_persistent(stream)
+            _lib.check(rc)
+
+    def token_persistent_checked(self, x_tok: torch.Tensor, stream=None):
+        """One token by an ordinary launch, checked; if its grid was not
+        resident at once, the token runs again by a cooperative launch.
+        Synchronises `stream` (one host round trip per token)."""
+        self.token_persistent(x_tok, stream, ordinary=True)
+        try:
+            self.check_persistent(stream)
+        except _lib.MoeError as e:
+            if e.code != _lib.MOE_ERR_TIMEOUT:
+                raise
+            self.token_persistent(x_tok, stream, ordinary=False)
+            self.check_persistent(stream)
+            return "cooperative"
+        return "ordinary"
 
     # -- bookkeeping --------------------------------------------------------
     def expert_bytes_per_token(self) -> int:
@@ -269,7 +324,7 @@ class StreamingStack:
         self.device = _norm_device(device)
         self.store = host_store if host_store is not None else \
             synth.make_host_store(geom, n_layers * self.E, self.device, seed)
-        self.pool = ExpertPool(geom, n_slots, self.store, self.device, evict=evict,
+        self.pool = ExpertPool(geom, n_slots, store=self.store, device=self.device, evict=evict,
                                widen=widen, n_layers=n_layers)
         self.W, self.bias, self.logpop = routers(geom, n_layers, self.device, seed,
                                                  zipf_s, router_bias)

@@ -155,14 +155,46 @@ class ExpertStoreFile:
     def record(self, layer: int, expert: int) -> np.ndarray:
         return self.records[layer * self.index.n_experts + expert]
 
-    def to_host_store(self, chunk_records: int = 64):
-        """Copy every record into pinned host memory (the pool's fill source)."""
+    def to_host_store(self, chunk_records: int = 64, n_workers: int = 1):
+        """Read every record into pinned host memory (the pool's fill source)."""
         from .pool import HostStore
         hs = HostStore(self.geom, self.n_records)
-        for r0 in range(0, self.n_records, chunk_records):
-            r1 = min(self.n_records, r0 + chunk_records)
-            hs.array[r0:r1] = self.records[r0:r1]
+        self.read_into(hs.array, chunk_records, n_workers)
         return hs
+
+    def read_into(self, dst: np.ndarray, chunk_records: int = 64, n_workers: int = 1):
+        """Read every record into dst (uint8 [n_records, blob_bytes], C order):
+        contiguous preadv calls of `chunk_records` records straight into it,
+        on `n_workers` threads (preadv releases the GIL), as the reference's
+        fill workers read (engine_v3.py:255-290)."""
+        from concurrent.futures import ThreadPoolExecutor
+        rb = self.index.blob_bytes
+        if dst.dtype != np.uint8 or dst.shape != (self.n_records, rb) or \
+                not dst.flags.c_contiguous:
+            raise ValueError(f"dst must be C-contiguous uint8 {(self.n_records, rb)}")
+        fd = os.open(os.path.join(self.dir, BLOB), os.O_RDONLY)
+
+        def read(r0):
+            r1 = min(self.n_records, r0 + chunk_records)
+            view = memoryview(dst[r0:r1].reshape(-1))
+            want, got = (r1 - r0) * rb, 0
+            while got < want:
+                n = os.preadv(fd, [view[got:]], r0 * rb + got)
+                if n <= 0:
+                    raise IOError(f"short read {got} of {want} at record {r0}")
+                got += n
+
+        try:
+            starts = range(0, self.n_records, chunk_records)
+            if n_workers <= 1:
+                for r0 in starts:
+                    read(r0)
+            else:
+                with ThreadPoolExecutor(n_workers, thread_name_prefix="fetch") as ex:
+                    list(ex.map(read, starts))
+        finally:
+            os.close(fd)
+        return dst
 
     def to_device(self, device="cuda", chunk_records: int = 64):
         """Copy every record into an HBM store tensor [n_records, blob_bytes]."""

@@ -38,7 +38,7 @@ def _blocks(geom, pool, W):
 
 
 def _run(geom, store, W, xs, n_slots):
-    pool = ExpertPool(geom, n_slots, store, n_layers=L)
+    pool = ExpertPool(geom, n_slots, store=store, n_layers=L)
     blocks = _blocks(geom, pool, W)
     ys = []
     for t in range(xs.shape[0]):
@@ -101,7 +101,7 @@ def test_prefill_through_the_block(world):
     geom, store, W, _, host = world
     # room for layer 1's experts and the lookahead's prefetch of layer 2
     # (each up to all 128 over 40 tokens), both issued before the acquire
-    pool = ExpertPool(geom, 300, store, n_layers=L)
+    pool = ExpertPool(geom, 300, store=store, n_layers=L)
     blocks = _blocks(geom, pool, W)
     xs = synth.hidden_states(40, L, geom.d_model, "cuda", 20260504)
     x = xs[:, 1].contiguous()                     # 40 tokens at layer 1

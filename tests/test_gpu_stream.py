@@ -122,7 +122,7 @@ def test_on_disk_store_feeds_the_pool(tmp_path):
     xs = synth.hidden_states(3, geom.n_layers, geom.d_model, "cuda", 20260605)
     outs = []
     for src in (host, recs):
-        pool = ExpertPool(geom, 16, src, n_layers=geom.n_layers)
+        pool = ExpertPool(geom, 16, store=src, n_layers=geom.n_layers)
         blocks = []
         for i in range(geom.n_layers):
             blocks.append(MoEBlock(i, geom, pool, W[i], None, blocks))
@@ -131,3 +131,34 @@ def test_on_disk_store_feeds_the_pool(tmp_path):
     for a, b in zip(*outs):
         assert torch.equal(a, b)
     host.close()
+
+
+def test_expert_pool_reference_constructor(tmp_path):
+    """ExpertPool(model_dir, n_slots, n_workers), the reference's signature
+    (engine_v3.py:128): the store directory is read into pinned memory by the
+    workers, acquire fills the pool from it byte for byte, and stats() has
+    the reference's keys (engine_v3.py:456-464) with the fill telemetry."""
+    from test_pool_host import REFERENCE_STATS_KEYS
+    geom = G.SMALL
+    recs = synth.make_store(geom, geom.n_layers * geom.n_experts, "cuda", 20260621)
+    S.write_store(str(tmp_path), geom, recs.cpu().numpy())
+    pool = ExpertPool(str(tmp_path), 12, 3)
+    assert pool.n_slots == 12 and pool.n_workers == 3 and pool.n_layers == geom.n_layers
+    assert pool.blob == geom.record_bytes and pool.group_size == 64 and pool.bits == 4
+    pool.prefetch(1, [4, 5])
+    slots = pool.acquire(0, [3, 7, 9])
+    slots1 = pool.acquire(1, [4, 5, 6])
+    torch.cuda.synchronize()
+    for layer, es, ss in ((0, [3, 7, 9], slots), (1, [4, 5, 6], slots1)):
+        for e, sl in zip(es, ss):
+            got = pool.read_slot(sl)
+            for c in geom.components:
+                want = recs[layer * geom.n_experts + e, c.offset:c.offset + c.nbytes]
+                assert torch.equal(got[c.name].contiguous().view(torch.uint8).reshape(-1),
+                                   want.cpu()), (layer, e, c.name)
+    s = pool.stats()
+    assert set(s) == REFERENCE_STATS_KEYS
+    assert s["total"] == 6 and s["miss"] == 4 and s["prefetch"] == 2
+    assert s["blocked"] >= 0.0 and s["busy_s"] > 0.0 and s["depth"] >= 1.0
+    assert abs(s["gb"] * 2 ** 30 - 6 * geom.record_bytes) < 1
+    pool.store.close()

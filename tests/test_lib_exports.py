@@ -95,7 +95,7 @@ def _qwen3_view(pad=0, swap_store=False):
 def _stack_call(lib, g, v):
     return lib.moe_stack_decode(C.byref(v), C.byref(g.c_geom()), 48, 128, 8, None, None,
                                 None, 0, 1, 8, None, None, None, None, None, None, None,
-                                1, None, 0, None)
+                                1, 0, None, 0, None)
 
 
 def test_persistent_decode_requires_the_packed_pool_layout():
@@ -117,3 +117,60 @@ def test_persistent_decode_requires_the_packed_pool_layout():
     # the packed layout passes this check; the next argument error reports
     g, v = _qwen3_view()
     assert _stack_call(lib, g, v) == _lib.MOE_ERR_INVALID
+
+
+def _stack_args(lib, g, v, epoch=1, flags=0, n_layers=48):
+    """Every argument of moe_stack_decode valid (made-up, never dereferenced
+    device addresses) except what a test changes."""
+    fake = 0x30_0000_0000
+    ws_bytes = lib.moe_stack_workspace(C.byref(g.c_geom()), n_layers, 128, 8)
+    return (C.byref(v), C.byref(g.c_geom()), n_layers, 128, 8, fake, fake, None, 0, 1, 8,
+            fake, fake, fake, fake, fake, fake, fake, epoch, flags, fake, ws_bytes, None)
+
+
+def test_persistent_decode_flags_and_epoch_bound():
+    """Unknown launch flags are rejected; the epoch must start at 1 and stay
+    below the bound that keeps the per-layer flags (epoch * n_layers + l)
+    inside 32 bits -- past it the caller zeroes the workspace and restarts."""
+    lib = _lib.lib()
+    g, v = _qwen3_view()
+    assert lib.moe_stack_decode(*_stack_args(lib, g, v, flags=4)) == _lib.MOE_ERR_INVALID
+    assert b"unknown flags" in lib.moe_last_error()
+    assert lib.moe_stack_decode(*_stack_args(lib, g, v, epoch=0)) == _lib.MOE_ERR_INVALID
+    assert b"epoch must start at 1" in lib.moe_last_error()
+    last_ok = (2 ** 32 - 1) // 48 - 1          # (epoch + 1) * 48 <= 2^32 - 1
+    assert lib.moe_stack_decode(*_stack_args(lib, g, v, epoch=last_ok + 1)) == \
+        _lib.MOE_ERR_INVALID
+    assert b"too large" in lib.moe_last_error()
+    # the DecodeStack restarts well before that bound
+    from moe_stream_amd.stack import DecodeStack
+    for L in (1, 48, 4096, 2 ** 20):
+        lim = DecodeStack.epoch_limit(L)
+        assert lim >= 1 and (lim + 1) * L <= 2 ** 32 - 1
+
+
+def test_fill_slots_range_checks_records_and_slots():
+    """Record indices are checked against the source store's record count
+    and slots against the pool on the host, before anything is enqueued."""
+    lib = _lib.lib()
+    g, v = _qwen3_view()
+    recs = (C.c_int64 * 2)(0, 16)          # the view's store holds 16 records
+    slots = (C.c_int32 * 2)(0, 1)
+    assert lib.moe_fill_slots(C.byref(v), None, 0, 0, recs, slots, 2, None) == \
+        _lib.MOE_ERR_INVALID
+    assert b"record 16 outside [0, 16)" in lib.moe_last_error()
+    src = 0x40_0000_0000
+    rb = g.record_bytes
+    assert lib.moe_fill_slots(C.byref(v), src, rb, 10, recs, slots, 2, None) == \
+        _lib.MOE_ERR_INVALID
+    assert b"record 16 outside [0, 10)" in lib.moe_last_error()
+    recs[1] = -1
+    assert lib.moe_fill_slots(C.byref(v), src, rb, 10, recs, slots, 2, None) == \
+        _lib.MOE_ERR_INVALID
+    recs[1] = 3
+    slots[1] = 8                            # 8 slots in the view
+    assert lib.moe_fill_slots(C.byref(v), src, rb, 10, recs, slots, 2, None) == \
+        _lib.MOE_ERR_INVALID
+    assert b"slot 8 outside [0, 8)" in lib.moe_last_error()
+    assert lib.moe_fill_slots(C.byref(v), src, rb, 0, recs, slots, 2, None) == \
+        _lib.MOE_ERR_INVALID

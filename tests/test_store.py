@@ -144,3 +144,19 @@ def test_repack_rejects_wrong_shapes(tmp_path):
     _write_safetensors(src / "m.safetensors", tens)
     with pytest.raises(S.StoreFormatError, match="up_proj.scales"):
         S.repack_safetensors(str(src), str(tmp_path / "out"), geom)
+
+
+def test_read_into_matches_the_records(tmp_path):
+    """The pinned-store load of ExpertPool(model_dir, n_slots, n_workers):
+    chunked preadv straight into the destination, on several workers, with a
+    last chunk shorter than the others."""
+    geom = G.SMALL
+    recs = _small_records(geom, seed=3)
+    S.write_store(str(tmp_path), geom, recs)
+    f = S.ExpertStoreFile(str(tmp_path), base=G.SMALL)
+    for workers, chunk in ((1, 64), (3, 7), (8, 1)):
+        dst = np.zeros_like(recs)
+        f.read_into(dst, chunk_records=chunk, n_workers=workers)
+        np.testing.assert_array_equal(dst, recs)
+    with pytest.raises(ValueError):
+        f.read_into(np.zeros((3, geom.record_bytes), dtype=np.uint8))
