@@ -77,6 +77,13 @@ int check_packed_layout(const moe_pool_view *v, const moe_geom *g) {
       return fail(MOE_ERR_UNSUPPORTED,
                   "persistent decode needs repacked records: component %d at %lld != %lld", c,
                   (long long)v->comp_offset[c], (long long)off);
+    if (v->n_slots > 0 &&
+        static_cast<const char *>(v->base[c]) !=
+            static_cast<const char *>(v->base[0]) + (int64_t)v->n_slots * off)
+      return fail(MOE_ERR_UNSUPPORTED,
+                  "persistent decode needs the pool's component arrays in one allocation, "
+                  "back to back: component %d is not at base[0] + n_slots * %lld", c,
+                  (long long)off);
     off += cb[c];
   }
   const int64_t rec = (off + 16383) / 16384 * 16384;
@@ -373,14 +380,12 @@ int moe_stack_trace(void *device_buf, size_t bytes) {
 }
 
 size_t moe_stack_workspace(const moe_geom *g, int32_t n_layers, int32_t E, int32_t k) {
-  if (!g || n_layers <= 0 || E <= 0 || k <= 0) return 0;
-  const size_t abort_w = 256;   // the launch's abort word, on a line of its own
-  const size_t counters = (size_t)n_layers * moe::kCountersPerLayer * moe::kCounterWords * 4;
-  const size_t logits = ((size_t)2 * E * 8 + 255) & ~(size_t)255;   // flagged entries
-  // flagged activations (2 bf16 + flag per 8 bytes): predicted (+ spares), fix-up
-  const size_t hp = ((size_t)(k + moe::kSpare) * (g->d_ff / 2) * 8 + 255) & ~(size_t)255;
-  const size_t hf = ((size_t)k * (g->d_ff / 2) * 8 + 255) & ~(size_t)255;
-  return abort_w + counters + logits + hp + hf;
+  if (!g || n_layers <= 0 || E <= 0 || E > moe::kRouteMaxE || k <= 0) return 0;
+  // (the workspace does not depend on the routing rule: any instantiation)
+  const moe::StackLaunch *S =
+      moe::find_stack(g->d_model, g->d_ff, k, g->has_proj_bias, g->act, -1, 0);
+  if (!S) return 0;
+  return S->ws_fixed + (size_t)n_layers * moe::kStackCounterBytesPerLayer;
 }
 
 int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_layers,
@@ -393,11 +398,13 @@ int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_lay
   moe::PoolArgs pa;
   int rc = make_pool_args(pool, g, &pa);
   if (rc) return rc;
-  const moe::StackLaunch *S = moe::find_stack(g->d_model, g->d_ff, k, g->has_proj_bias);
+  const moe::StackLaunch *S =
+      moe::find_stack(g->d_model, g->d_ff, k, g->has_proj_bias, g->act, mode, renorm);
   if (!S)
     return fail(MOE_ERR_UNSUPPORTED,
-                "no persistent decode kernel for d_model=%d d_ff=%d k=%d proj_bias=%d",
-                g->d_model, g->d_ff, k, g->has_proj_bias);
+                "no persistent decode kernel for d_model=%d d_ff=%d k=%d proj_bias=%d act=%d "
+                "routing=%d renorm=%d", g->d_model, g->d_ff, k, g->has_proj_bias, g->act, mode,
+                renorm);
   rc = check_packed_layout(pool, g);
   if (rc) return rc;
   if (n_layers <= 0) return fail(MOE_ERR_INVALID, "n_layers=%d", n_layers);
@@ -422,9 +429,11 @@ int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_lay
   if ((uint64_t)epoch * (uint64_t)n_layers + (uint64_t)n_layers > 0xffffffffull)
     return fail(MOE_ERR_INVALID, "epoch %u too large for %d layers: zero the workspace and "
                 "restart at 1", epoch, n_layers);
-  char *ws = static_cast<char *>(workspace);
   moe::StackArgs a;
-  a.pa = pa;
+  a.sp.slots = pa.n_slots > 0 ? pa.base[0] : nullptr;
+  a.sp.store = pa.store;
+  a.sp.n_slots = pa.n_slots;
+  a.sp.n_records = pa.n_records;
   a.x = x;
   a.W = W;
   a.bias = bias;
@@ -435,15 +444,7 @@ int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_lay
   a.refs_out = slot_refs;
   a.pred = pred;
   a.miss = miss_count;
-  a.abort_w = reinterpret_cast<uint32_t *>(ws);
-  ws += 256;
-  a.cnt = reinterpret_cast<uint32_t *>(ws);
-  ws += (size_t)n_layers * moe::kCountersPerLayer * moe::kCounterWords * 4;
-  a.lgt = reinterpret_cast<uint64_t *>(ws);
-  ws += ((size_t)2 * E * 8 + 255) & ~(size_t)255;
-  a.hpred = reinterpret_cast<uint64_t *>(ws);
-  ws += ((size_t)(k + moe::kSpare) * (g->d_ff / 2) * 8 + 255) & ~(size_t)255;
-  a.hfix = reinterpret_cast<uint64_t *>(ws);
+  a.ws = static_cast<char *>(workspace);
   a.L = n_layers;
   a.E = E;
   a.kp = k_pred;

@@ -79,10 +79,13 @@ void launch_grouped(const GroupedLaunch *G, const PoolArgs &pa, const int32_t *r
 // ---- whole-token persistent decode (stack_decode.hip) ---------------------
 struct StackArgs;
 struct StackLaunch {
-  int d_model, d_ff, k, has_bias, nwg;
+  int d_model, d_ff, k, has_bias, act, mode, renorm, nwg;
+  size_t ws_fixed;   // workspace bytes before the per-layer counters
   const void *func;
 };
-const StackLaunch *find_stack(int d_model, int d_ff, int k, int has_bias);
+constexpr size_t kStackCounterBytesPerLayer = 8 * 32 * 4;   // kSub lines of 32 words
+const StackLaunch *find_stack(int d_model, int d_ff, int k, int has_bias, int act, int mode,
+                              int renorm);
 hipError_t launch_stack(const StackLaunch *S, StackArgs &a, bool ordinary, hipStream_t s);
 void launch_slot_lookup(const int32_t *table, int E, const int32_t *ids, int n,
                         int32_t *refs, int32_t *miss_count, hipStream_t s);

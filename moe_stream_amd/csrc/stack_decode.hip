@@ -41,6 +41,7 @@
 // engine_120b.py:65-70), top_k_indices (engine_v3.py:476-483), slot lookup
 // (engine_v3.py:548-552), the expert block (engine_v3.py:588-600).
 #include <atomic>
+#include <cstddef>
 
 #include "launchers.h"
 
@@ -48,8 +49,44 @@ namespace moe {
 
 constexpr uint32_t kSpinLimit = 1u << 20;
 
+// The pool as this kernel sees it: the packed layout of one geometry with
+// every component array in ONE allocation, back to back in component order
+// (component c's [n_slots, *shape] array at slots + n_slots * offset of c in
+// a record), so one base address stands for all of them; and the store of
+// repacked records.  Few scalar registers: the kernel runs at the limit.
+struct StackPool {
+  const char *slots;
+  const char *store;
+  int32_t n_slots;
+  int32_t n_records;
+};
+
+// resolve() for a StackPool in the packed layout L; nullptr when the
+// reference is out of range.
+template <class L>
+__device__ __forceinline__ const char *resolve_stack(const StackPool &sp, int c, int32_t ref) {
+  if (ref >= 0) {
+    if (ref >= sp.n_slots) return nullptr;
+    return sp.slots + (int64_t)sp.n_slots * L::comp_offset(c) + (int64_t)ref * L::slot_bytes(c);
+  }
+  const int64_t r = -(int64_t)ref - 1;
+  if (sp.store == nullptr || r >= sp.n_records) return nullptr;
+  return sp.store + r * L::kRecordBytes + L::comp_offset(c);
+}
+// As resolve_stack, but an out-of-range reference reads slot 0 (or store
+// record 0 when there are no slots) and clears `ok`.
+template <class L>
+__device__ __forceinline__ const char *resolve_stack_safe(const StackPool &sp, int c,
+                                                          int32_t ref, bool &ok) {
+  const char *p = resolve_stack<L>(sp, c, ref);
+  ok = p != nullptr;
+  return ok ? p
+            : (sp.n_slots > 0 ? sp.slots + (int64_t)sp.n_slots * L::comp_offset(c)
+                              : sp.store + L::comp_offset(c));
+}
+
 struct StackArgs {
-  PoolArgs pa;
+  StackPool sp;
   const uint16_t *x;      // [L][D] bf16 layer inputs
   const uint16_t *W;      // [L][E][D] bf16 routers
   const uint16_t *bias;   // [L][E] bf16 or null
@@ -60,16 +97,28 @@ struct StackArgs {
   int32_t *refs_out;      // [L][K]
   int32_t *pred;          // [L][KP]
   int32_t *miss;          // [L]
-  uint64_t *lgt;          // ws [2][E] router / lookahead logits, flagged (put_logit)
-  uint64_t *hpred;        // ws [K + kSpare][F/2] activations of the predicted experts and
-  uint64_t *hfix;         // ws [K][F/2] of the fix-up slots: 2 bf16 + layer flag each
-  uint32_t *cnt;          // ws [L][kSub] counters, 128 B apart
-  uint32_t *abort_w;      // ws: epoch of the launch in which a wait gave up
+  char *ws;               // workspace (StackWs layout)
   int L, E, kp, mode, renorm, act;
   float alpha, limit;
   uint32_t epoch;
   uint64_t *trace;        // optional [kTraceWGs][L][kTracePoints] wall clock
 };
+
+// A field of the kernel's only argument (StackArgs, at offset 0 of the
+// kernarg segment), read from the kernarg segment where it is used: the
+// opaque offset keeps the compiler from loading it once and holding it in
+// scalar registers for the whole kernel (this kernel runs at the scalar
+// register limit, and a value held that way is spilled).  For fields the
+// hot loops do not touch.
+template <class T>
+__device__ __forceinline__ T karg_load(size_t off) {
+  typedef __attribute__((address_space(4))) const char kchar;
+  typedef __attribute__((address_space(4))) const T kT;
+  kchar *p = (kchar *)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(off));
+  return *reinterpret_cast<kT *>(p + off);
+}
+#define KARG(field) karg_load<decltype(StackArgs::field)>(offsetof(StackArgs, field))
 
 // Phase trace: wall-clock stamps of thread 0 of the first kTraceWGs
 // workgroups at each phase boundary of each layer.
@@ -80,17 +129,19 @@ enum { TR_START, TR_R_WAITED, TR_R_ARRIVED, TR_SELECTED, TR_U_ARRIVED,
 
 // Called by one wave at a time; its lane 0 stamps.
 __device__ __forceinline__ void trace_mark(const StackArgs &a, int l, int point) {
-  if (a.trace && blockIdx.x < kTraceWGs && (threadIdx.x & 63) == 0)
-    a.trace[((size_t)blockIdx.x * a.L + l) * kTracePoints + point] = wall_clock64();
+  uint64_t *tr = KARG(trace);
+  if (tr && blockIdx.x < kTraceWGs && (threadIdx.x & 63) == 0)
+    tr[((size_t)blockIdx.x * a.L + l) * kTracePoints + point] = wall_clock64();
 }
 // Stamp once `dep` has been computed (keeps the clock read after its inputs).
 __device__ __forceinline__ void trace_mark_after(const StackArgs &a, int l, int point,
                                                  float dep) {
-  if (a.trace && blockIdx.x < kTraceWGs && (threadIdx.x & 63) == 0) {
+  uint64_t *tr = KARG(trace);
+  if (tr && blockIdx.x < kTraceWGs && (threadIdx.x & 63) == 0) {
     __builtin_amdgcn_s_waitcnt(0);
     uint64_t t = wall_clock64();
     if (dep == 1.2345e-37f) t = 0;   // data dependence only
-    a.trace[((size_t)blockIdx.x * a.L + l) * kTracePoints + point] = t;
+    tr[((size_t)blockIdx.x * a.L + l) * kTracePoints + point] = t;
   }
 }
 
@@ -108,6 +159,8 @@ constexpr int kSpare = 2;
 // logits and expert activations carry their own flags instead.
 enum { CNT_D = 0 };
 constexpr int kCountersPerLayer = 1;
+static_assert(kStackCounterBytesPerLayer == (size_t)kCountersPerLayer * kCounterWords * 4,
+              "host-side workspace size");
 
 // The flag a data entry exchanged between workgroups carries (router logits,
 // expert activations): unique per (token, layer), so an entry left by an
@@ -125,26 +178,55 @@ __device__ __forceinline__ void put_logit(uint64_t *slot, float v, uint32_t fl) 
                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The workspace: one base address, the parts at offsets fixed by the
+// geometry (the counters, whose size depends on the layer count, last).
+//   abort word (256 B) | router + lookahead logits [2][kRouteMaxE], flagged
+//   8-byte entries | activations of the predicted and spare experts
+//   [K + kSpare][F/2] and of the fix-up slots [K][F/2] (2 bf16 + layer flag
+//   per 8 bytes) | counters [L][kSub], 128 B apart
+template <int F, int K>
+struct StackWs {
+  static constexpr size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
+  static constexpr size_t kAbort = 0;
+  static constexpr size_t kLgt = 256;
+  static constexpr size_t kHpred = kLgt + al((size_t)2 * kRouteMaxE * 8);
+  static constexpr size_t kHfix = kHpred + al((size_t)(K + kSpare) * (F / 2) * 8);
+  static constexpr size_t kCnt = kHfix + al((size_t)K * (F / 2) * 8);
+  static constexpr size_t bytes(int L) {
+    return kCnt + (size_t)L * kCountersPerLayer * kCounterWords * 4;
+  }
+};
+
+template <class W>
 __device__ __forceinline__ uint32_t *counter(const StackArgs &a, int l, int which) {
-  return a.cnt + ((size_t)l * kCountersPerLayer + which) * kCounterWords;
+  return reinterpret_cast<uint32_t *>(a.ws + W::kCnt) +
+         ((size_t)l * kCountersPerLayer + which) * kCounterWords;
 }
 
 // The launch's abort word (in the workspace): the epoch of the launch in
-// which some wait gave up.  Every poll loads it in the same batch as its own
-// loads (a poll that misses costs one round trip, not a second one for this
-// check), so once one wait has timed out the others stop at their next miss
-// instead of each running to the spin limit.  A value left by an earlier
-// launch never equals the current epoch, so it cannot cut a new launch short.
+// which some wait gave up.  A wait that keeps missing loads it every 64th
+// poll (a normal wait ends long before, so it costs the fast path nothing),
+// so once one wait has timed out the others stop soon instead of each
+// running to the spin limit.  A value left by an earlier launch never equals
+// the current epoch, so it cannot cut a new launch short.
 struct Abort {
   uint32_t *word;
   uint32_t ep;
-  __device__ __forceinline__ uint32_t load() const {
-    return __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  // one lane: this launch gives up (and the device error word says why)
-  __device__ __forceinline__ void raise() const {
-    __hip_atomic_store(word, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    flag_timeout();
+  // One whole wave, after its `spins`-th missed poll: true when it must stop
+  // waiting (this launch gave up, or this wait ran past the spin limit).
+  __device__ __forceinline__ bool gave_up(uint32_t spins) const {
+    if ((spins & 63) == 0) {
+      const uint32_t w = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__builtin_amdgcn_readfirstlane(w) == ep) return true;
+    }
+    if (spins > kSpinLimit) {
+      if ((threadIdx.x & 63) == 0) {
+        __hip_atomic_store(word, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        flag_timeout();
+      }
+      return true;
+    }
+    return false;
   }
 };
 
@@ -158,18 +240,13 @@ __device__ __forceinline__ void wave_wait(const uint32_t *c, uint32_t target, co
     int v = (lane < kSub) ? (int)__hip_atomic_load(c + lane * 32, __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT)
                           : 0;
-    const uint32_t abw = ab.load();
     v += dpp_i<kDppQuadXor1>(v);
     v += dpp_i<kDppQuadXor2>(v);
     v += dpp_i<kDppHalfMirror>(v);
     const uint32_t sum = (uint32_t)__builtin_amdgcn_readfirstlane(v);
     // counters are monotonic modulo 2^32: compare the distance, not the values
     if ((int32_t)(sum - target) >= 0) break;
-    if (__builtin_amdgcn_readfirstlane(abw) == ab.ep) break;   // another wait gave up
-    if (++spins > kSpinLimit) {
-      if (lane == 0) ab.raise();
-      break;
-    }
+    if (ab.gave_up(++spins)) break;
     __builtin_amdgcn_s_sleep(1);
   }
 }
@@ -185,16 +262,11 @@ __device__ __forceinline__ void get_logits(const uint64_t *slots, int n, uint32_
   while (true) {
     const uint64_t v0 = __hip_atomic_load(p0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint64_t v1 = __hip_atomic_load(p1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t abw = ab.load();
     const bool ok = (e0 >= n || (uint32_t)(v0 >> 32) == fl) && (e1 >= n || (uint32_t)(v1 >> 32) == fl);
     z0 = __uint_as_float((uint32_t)v0);
     z1 = __uint_as_float((uint32_t)v1);
     if (__ballot(!ok) == 0) break;
-    if (__builtin_amdgcn_readfirstlane(abw) == ab.ep) break;   // another wait gave up
-    if (++spins > kSpinLimit) {
-      if (lane == 0) ab.raise();
-      break;
-    }
+    if (ab.gave_up(++spins)) break;
     __builtin_amdgcn_s_sleep(1);
   }
 }
@@ -229,9 +301,9 @@ __device__ __forceinline__ void wg_arrive(uint32_t *c) {
                            __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int D, int F, int K, bool PBIAS>
+template <int D, int F, int K, bool PBIAS, int ACT, int MODE, int RENORM>
 struct StackCfg {
-  static constexpr int D_ = D, F_ = F, K_ = K;
+  static constexpr int D_ = D, F_ = F, K_ = K, ACT_ = ACT, MODE_ = MODE, RENORM_ = RENORM;
   static constexpr bool PBIAS_ = PBIAS;
   using Layout = PackedLayout<D, F, PBIAS>;   // the pool layout the kernel requires
   static constexpr int NT = 512;                 // 8 waves
@@ -255,6 +327,14 @@ struct StackCfg {
   static_assert(K <= 8, "one wave per expert in the down phase");
   static_assert((ROWS_U * NG * 2) % 16 == 0 && (ROWS_D * NGF * 2) % 16 == 0, "scale blocks");
 };
+
+// The gated activation of the kernel's instantiation; the clamped form's
+// alpha and limit come from the kernarg segment where they are used.
+template <class C>
+__device__ __forceinline__ float stack_act(float g, float u) {
+  if (C::ACT_ == MOE_ACT_SWIGLU) return apply_act(MOE_ACT_SWIGLU, g, u, 0.f, 0.f);
+  return apply_act(MOE_ACT_SWIGLU_CLAMP, g, u, KARG(alpha), KARG(limit));
+}
 
 // One whole wave, one row per 16 lanes (the row's activation in `hb` on
 // each of its lanes): the 4 rows' bf16 activations as two flagged 8-byte
@@ -286,7 +366,7 @@ __device__ __forceinline__ uint32_t u_rows(const StackArgs &a, int32_t ref, int 
   constexpr int SB_U4 = C::SB_U4, NP = C::NP;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int uj = lane % SGU, usub = lane / SGU;
-  const bool ok = resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref) != nullptr;
+  const bool ok = resolve_stack<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_W, NP), ref) != nullptr;
   const int urow = row0 + wave * RPSU + usub;
   float pg = 0.f, pu = 0.f;
   if (ok) {
@@ -311,11 +391,11 @@ __device__ __forceinline__ uint32_t u_rows(const StackArgs &a, int32_t ref, int 
   if (ok) {
     if (C::PBIAS_) {
       pg += bf16_to_f32(reinterpret_cast<const uint16_t *>(
-          resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref))[urow]);
+          resolve_stack<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_BIAS, NP), ref))[urow]);
       pu += bf16_to_f32(reinterpret_cast<const uint16_t *>(
-          resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref))[urow]);
+          resolve_stack<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_BIAS, NP), ref))[urow]);
     }
-    hb = f32_to_bf16(apply_act(a.act, pg, pu, a.alpha, a.limit));
+    hb = f32_to_bf16(stack_act<C>(pg, pu));
   } else if (lane == 0) {
     flag_error();
   }
@@ -352,7 +432,7 @@ __device__ __forceinline__ uint32_t task_rows(const StackArgs &a, int32_t ref, b
   pg = group_sum<SGU>(pg) + gbv;
   pu = group_sum<SGU>(pu) + ubv;
   uint32_t hb = 0;
-  if (ok) hb = f32_to_bf16(apply_act(a.act, pg, pu, a.alpha, a.limit));
+  if (ok) hb = f32_to_bf16(stack_act<C>(pg, pu));
   else if (lane == 0) flag_error();
   return hb;
 }
@@ -371,12 +451,12 @@ struct TaskRegs {
     static_assert(C::RPSU == 4 && SGU == 16 && NG * 2 * 4 == 16 * 16,
                   "a task: 4 rows of 16 lanes; its scales: 4 arrays of 16 pieces");
     const int lane = threadIdx.x & 63, uj = lane % SGU, usub = lane / SGU;
-    const char *gw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
-    const char *uw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
-    const char *gs = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok);
-    const char *gb = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok);
-    const char *us = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok);
-    const char *ub = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok);
+    const char *gw = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
+    const char *uw = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_W, NP), ref, ok);
+    const char *gs = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_S, NP), ref, ok);
+    const char *gb = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_B, NP), ref, ok);
+    const char *us = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_S, NP), ref, ok);
+    const char *ub = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_B, NP), ref, ok);
     const int arr = lane >> 4, row = 4 * b + usub;
     const char *sa = arr == 0 ? gs : arr == 1 ? gb : arr == 2 ? us : ub;
     sv = load16(reinterpret_cast<const uint4 *>(sa + (int64_t)(4 * b) * NG * 2) + (lane & 15));
@@ -384,9 +464,9 @@ struct TaskRegs {
     if (C::PBIAS_) {
       bool okb;
       gbv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-          resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[row]);
+          resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[row]);
       ubv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-          resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[row]);
+          resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[row]);
     }
     issue_order_fence();
     const uint4 *g4 = reinterpret_cast<const uint4 *>(gw + (int64_t)row * (D / 2)) + uj;
@@ -427,12 +507,12 @@ __device__ __forceinline__ bool task_stage_lds(const StackArgs &a, int32_t ref, 
   typedef __attribute__((address_space(3))) void lds_void;
   const int lane = threadIdx.x & 63, uj = lane % SGU, usub = lane / SGU;
   bool ok;
-  const char *gw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
-  const char *uw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
-  const char *gs = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok);
-  const char *gb = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok);
-  const char *us = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok);
-  const char *ub = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok);
+  const char *gw = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
+  const char *uw = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_W, NP), ref, ok);
+  const char *gs = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_S, NP), ref, ok);
+  const char *gb = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_B, NP), ref, ok);
+  const char *us = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_S, NP), ref, ok);
+  const char *ub = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_B, NP), ref, ok);
   const int arr = lane >> 4, row = 4 * b + usub;
   const char *sa = arr == 0 ? gs : arr == 1 ? gb : arr == 2 ? us : ub;
   const uint4 *g4 = reinterpret_cast<const uint4 *>(gw + (int64_t)row * (D / 2)) + uj;
@@ -482,9 +562,9 @@ __device__ __forceinline__ uint32_t task_rows_lds(const StackArgs &a, int32_t re
   if (C::PBIAS_) {
     bool okb;
     gbv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-        resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[4 * b + usub]);
+        resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[4 * b + usub]);
     ubv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-        resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[4 * b + usub]);
+        resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[4 * b + usub]);
   }
   uint4 cg[CPLU], cu[CPLU];
 #pragma unroll
@@ -524,18 +604,13 @@ __device__ __forceinline__ void get_acts(const uint64_t *hf, uint32_t fl, const 
       v[q] = __hip_atomic_load(e0 + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       v[4 + q] = __hip_atomic_load(e1 + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    const uint32_t abw = ab.load();
     bool ok = true;
 #pragma unroll
     for (int q = 0; q < 8; ++q) ok = ok && (uint32_t)(v[q] >> 32) == fl;
     p0 = make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
     p1 = make_uint4((uint32_t)v[4], (uint32_t)v[5], (uint32_t)v[6], (uint32_t)v[7]);
     if (__ballot(!ok) == 0) break;
-    if (__builtin_amdgcn_readfirstlane(abw) == ab.ep) break;   // another wait gave up
-    if (++spins > kSpinLimit) {
-      if (lane == 0) ab.raise();
-      break;
-    }
+    if (ab.gave_up(++spins)) break;
     __builtin_amdgcn_s_sleep(1);
   }
 }
@@ -555,12 +630,12 @@ __device__ __forceinline__ void u_load(const StackArgs &a, int32_t ref, int row0
   // clamped index.
   ref = __builtin_amdgcn_readfirstlane(ref);
   bool ok;
-  const char *gw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
-  const char *uw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
-  const char *sb[4] = {resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok),
-                       resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok),
-                       resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok),
-                       resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok)};
+  const char *gw = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
+  const char *uw = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_W, NP), ref, ok);
+  const char *sb[4] = {resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_S, NP), ref, ok),
+                       resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_B, NP), ref, ok),
+                       resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_S, NP), ref, ok),
+                       resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_B, NP), ref, ok)};
 #pragma unroll
   for (int it = 0; it < C::SIT; ++it) {
     const int i = min(it * NT + tid, 4 * SB_U4 - 1);
@@ -591,9 +666,9 @@ __device__ __forceinline__ void d_load(const StackArgs &a, int32_t ref, int drow
   // (unconditional loads, as in u_load)
   ref = __builtin_amdgcn_readfirstlane(ref);
   bool ok;
-  const char *dw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_W, NP), ref, ok);
-  const char *ds = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_S, NP), ref, ok);
-  const char *db = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_B, NP), ref, ok);
+  const char *dw = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_DOWN, PART_W, NP), ref, ok);
+  const char *ds = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_DOWN, PART_S, NP), ref, ok);
+  const char *db = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_DOWN, PART_B, NP), ref, ok);
 #pragma unroll
   for (int it = 0; it < C::SDIT; ++it) {
     const int i = min(it * 64 + lane, 2 * SBD_U4 - 1);
@@ -607,9 +682,10 @@ __device__ __forceinline__ void d_load(const StackArgs &a, int32_t ref, int drow
     cd[i] = load_stream16(d4 + min(i * SGD + dj, UF - 1));
 }
 
-template <int D, int F, int K, bool PBIAS>
+template <int D, int F, int K, bool PBIAS, int ACT, int MODE, int RENORM>
 __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
-  using C = StackCfg<D, F, K, PBIAS>;
+  using C = StackCfg<D, F, K, PBIAS, ACT, MODE, RENORM>;
+  using WS = StackWs<F, K>;
   constexpr int NT = C::NT, U = C::U, SB_U4 = C::SB_U4;
   constexpr int UF = C::UF, NGF = C::NGF, SGD = C::SGD, CPLD = C::CPLD;
   constexpr int ROWS_D = C::ROWS_D, SBD_U4 = C::SBD_U4, NP = C::NP;
@@ -649,7 +725,10 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wg = blockIdx.x;
   const uint32_t ep = a.epoch;
-  const Abort ab{a.abort_w, ep};
+  const Abort ab{reinterpret_cast<uint32_t *>(a.ws + WS::kAbort), ep};
+  uint64_t *const lgt = reinterpret_cast<uint64_t *>(a.ws + WS::kLgt);
+  uint64_t *const hpred = reinterpret_cast<uint64_t *>(a.ws + WS::kHpred);
+  uint64_t *const hfix = reinterpret_cast<uint64_t *>(a.ws + WS::kHfix);
   const int upos = wg / NPOS, urow0 = (wg % NPOS) * ROWS_U;   // gate/up block
   const int drow0 = wg * ROWS_D;                               // down block
   const int dj = lane % SGD, dsub = lane / SGD;
@@ -673,7 +752,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
   for (int l = 0; l < a.L; ++l) {
     const bool has_next = l + 1 < a.L;
     const int nrows = a.E * (has_next ? 2 : 1);
-    const int32_t *tab = a.table + (size_t)l * a.E;
+    const int32_t *tab = KARG(table) + (size_t)l * a.E;
     if (wave == 0) trace_mark(a, l, TR_START);
     // the router row's weights before the wait (wave 6)
     uint4 wr[RIT];
@@ -682,7 +761,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
     if (rrow) {
       const int e = rnxt ? wg - a.E : wg;
       const uint4 *w4 =
-          reinterpret_cast<const uint4 *>(a.W + ((size_t)(rnxt ? l + 1 : l) * a.E + e) * D);
+          reinterpret_cast<const uint4 *>(KARG(W) + ((size_t)(rnxt ? l + 1 : l) * a.E + e) * D);
 #pragma unroll
       for (int it = 0; it < RIT; ++it) {
         const int i = lane + it * 64;
@@ -694,7 +773,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
     // flight here (loads complete in order, so a poll issued behind staging
     // loads would return only after them); it issues its own down staging
     // right after
-    if (l > 0) wg_wait(counter(a, l - 1, CNT_D), ep * C::ITEMS_D, W_RANK, ab);
+    if (l > 0) wg_wait(counter<WS>(a, l - 1, CNT_D), ep * C::ITEMS_D, W_RANK, ab);
     else __syncthreads();
     if (wave == 0) trace_mark(a, l, TR_R_WAITED);
     const int pcnt = pred_cnt[l & 1];
@@ -746,10 +825,10 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       uint32_t hs = 0;
       if (spare) hs = task_rows_lds<C>(a, sref, sok, ts % FT, spare_l[wave], act_l, asum_l);
       if (urows)
-        put_acts(a.hpred + (size_t)upos * (F / 2) + (urow0 + wave * C::RPSU) / 2, hu,
+        put_acts(hpred + (size_t)upos * (F / 2) + (urow0 + wave * C::RPSU) / 2, hu,
                  layer_flag(a, l));
       if (spare)
-        put_acts(a.hpred + (size_t)(K + ts / FT) * (F / 2) + 2 * (ts % FT), hs, layer_flag(a, l));
+        put_acts(hpred + (size_t)(K + ts / FT) * (F / 2) + 2 * (ts % FT), hs, layer_flag(a, l));
       if (wave == 0) trace_mark(a, l, TR_U_ARRIVED);
     } else if (wave == W_ROUTER) {
       // one router row (the lane partition and summation order of
@@ -772,19 +851,20 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
           acc = dot2_bf16(wr[it].w, v[it].w, acc);
         }
         acc = group_sum<64>(acc);
-        if (lane == 0) put_logit(a.lgt + (rnxt ? a.E : 0) + e, acc, layer_flag(a, l));
+        if (lane == 0) put_logit(lgt + (rnxt ? a.E : 0) + e, acc, layer_flag(a, l));
         trace_mark(a, l, TR_R_ARRIVED);
       }
       // lookahead ranking of layer l+1: raw bf16 logits of its router on x_l
       if (has_next) {
         const int e0 = lane, e1 = lane + 64;
-        const uint16_t *bias = a.bias ? a.bias + (size_t)(l + 1) * a.E : nullptr;
+        const uint16_t *bias0 = KARG(bias);
+        const uint16_t *bias = bias0 ? bias0 + (size_t)(l + 1) * a.E : nullptr;
         const float b0 = bias ? bf16_to_f32(bias[min(e0, a.E - 1)]) : 0.f;   // before the wait
         const float b1 = bias ? bf16_to_f32(bias[min(e1, a.E - 1)]) : 0.f;
-        const int32_t *tabn = a.table + (size_t)(l + 1) * a.E;
+        const int32_t *tabn = KARG(table) + (size_t)(l + 1) * a.E;
         const int32_t t0 = tabn[min(e0, a.E - 1)], t1 = tabn[min(e1, a.E - 1)];
         float l0, l1;
-        get_logits(a.lgt + a.E, a.E, layer_flag(a, l), ab, l0, l1);
+        get_logits(lgt + a.E, a.E, layer_flag(a, l), ab, l0, l1);
         const float z0 = e0 < a.E ? round_bf16(l0 + b0) : -INFINITY;
         const float z1 = e1 < a.E ? round_bf16(l1 + b1) : -INFINITY;
         bool s0, s1;
@@ -795,8 +875,9 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
         select_topk(e0 < a.E ? order_key(z0) : -1, e1 < a.E ? order_key(z1) : -1, ksel, lane,
                     s0, s1, r0, r1);
         if (wg == 0) {
-          if (s0 && r0 < a.kp) a.pred[(size_t)l * a.kp + r0] = e0;
-          if (s1 && r1 < a.kp) a.pred[(size_t)l * a.kp + r1] = e1;
+          int32_t *pred = KARG(pred);
+          if (s0 && r0 < a.kp) pred[(size_t)l * a.kp + r0] = e0;
+          if (s1 && r1 < a.kp) pred[(size_t)l * a.kp + r1] = e1;
         }
         int *pn = pred_buf[(l + 1) & 1];
         int32_t *pr = pred_ref[(l + 1) & 1];
@@ -816,19 +897,20 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
     } else {
       // ---- routing: every workgroup ranks this layer's logits ----------
       const int e0 = lane, e1 = lane + 64;
-      const uint16_t *bias = a.bias ? a.bias + (size_t)l * a.E : nullptr;
+      const uint16_t *bias0 = KARG(bias);
+      const uint16_t *bias = bias0 ? bias0 + (size_t)l * a.E : nullptr;
       const float b0 = bias ? bf16_to_f32(bias[min(e0, a.E - 1)]) : 0.f;   // before the wait
       const float b1 = bias ? bf16_to_f32(bias[min(e1, a.E - 1)]) : 0.f;
       // every expert's slot ref, also before the wait (clamped, unconditional)
       const int32_t t0 = tab[min(e0, a.E - 1)], t1 = tab[min(e1, a.E - 1)];
       float l0, l1;
-      get_logits(a.lgt, a.E, layer_flag(a, l), ab, l0, l1);
+      get_logits(lgt, a.E, layer_flag(a, l), ab, l0, l1);
       trace_mark(a, l, TR_R_ALL);
       const float z0 = e0 < a.E ? round_bf16(l0 + b0) : -INFINITY;
       const float z1 = e1 < a.E ? round_bf16(l1 + b1) : -INFINITY;
       trace_mark_after(a, l, TR_LOGITS, z0 + z1);
       float v0 = z0, v1 = z1;
-      if (a.mode == MOE_ROUTE_SOFTMAX_TOPK) {
+      if (MODE == MOE_ROUTE_SOFTMAX_TOPK) {
         const float m = wave_max(fmaxf(z0, z1));
         const float x0 = (e0 < a.E) ? expf(z0 - m) : 0.f;
         const float x1 = (e1 < a.E) ? expf(z1 - m) : 0.f;
@@ -843,8 +925,8 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
                   s0, s1, r0, r1);
       trace_mark_after(a, l, TR_TOPK, (float)(r0 + r1));
       float sc0 = v0, sc1 = v1;
-      if (a.mode == MOE_ROUTE_SOFTMAX_TOPK) {
-        if (a.renorm) {
+      if (MODE == MOE_ROUTE_SOFTMAX_TOPK) {
+        if (RENORM) {
           const float tot = round_bf16(group_sum<64>((s0 ? v0 : 0.f) + (s1 ? v1 : 0.f)));
           sc0 = round_bf16(v0 / tot);
           sc1 = round_bf16(v1 / tot);
@@ -925,10 +1007,10 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       staged[(l + 1) & 1] = 0;
     }
     if (wg == 0 && tid < K) {
-      a.ids[(size_t)l * K + tid] = sel_id[tid];
-      a.scores[(size_t)l * K + tid] = sel_sc[tid];
-      a.refs_out[(size_t)l * K + tid] = sel_ref[tid];
-      if (sel_ref[tid] < 0) atomicAdd(a.miss + l, 1);
+      KARG(ids)[(size_t)l * K + tid] = sel_id[tid];
+      KARG(scores)[(size_t)l * K + tid] = sel_sc[tid];
+      KARG(refs_out)[(size_t)l * K + tid] = sel_ref[tid];
+      if (sel_ref[tid] < 0) atomicAdd(KARG(miss) + l, 1);
     }
     // down rows of a routed expert that was not predicted: loaded now, so
     // their latency overlaps the fix-up pass
@@ -948,14 +1030,14 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       const int t = wave * NWG + wg;
       if (wave < C::WAVES_U && t < n_miss * FT)
         fix_task<C>(a, miss_ref[t / FT], t % FT, act_l, asum_l, hact_l[wave],
-                    a.hfix + (size_t)(t / FT) * (F / 2), layer_flag(a, l));
+                    hfix + (size_t)(t / FT) * (F / 2), layer_flag(a, l));
       if (wave == 0) trace_mark(a, l, TR_FIXED);
     }
     // ------------------------------------------------------------ D_l ----
     if (wave < K) {
       const int r = d_r, fx = d_fx;
       const int32_t dref = d_ref;
-      const char *dw = resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_W, NP), dref);
+      const char *dw = resolve_stack<typename C::Layout>(a.sp, comp_index(PROJ_DOWN, PART_W, NP), dref);
 
       uint4 *hact = hact_l[wave];
       float *hsum = hsum_l[wave];
@@ -971,9 +1053,9 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
         const int i0 = lane, i1 = lane + 64;
         uint4 p0, p1;
         const int src = fx < 0 ? 0 : miss_src[fx];
-        const uint64_t *hf = fx < 0    ? a.hpred + (size_t)wave * (F / 2)
-                             : src >= 0 ? a.hfix + (size_t)src * (F / 2)
-                                        : a.hpred + (size_t)(K - 1 - src) * (F / 2);
+        const uint64_t *hf = fx < 0    ? hpred + (size_t)wave * (F / 2)
+                             : src >= 0 ? hfix + (size_t)src * (F / 2)
+                                        : hpred + (size_t)(K - 1 - src) * (F / 2);
         get_acts<HU4>(hf, layer_flag(a, l), ab, p0, p1);
         if (wave == 0) trace_mark(a, l, TR_D_WAITED);
 #pragma unroll
@@ -1010,7 +1092,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       if (dj == 0) {
         if (PBIAS && dw != nullptr)
           p += bf16_to_f32(reinterpret_cast<const uint16_t *>(
-              resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_BIAS, NP), dref))[drow0 + dsub]);
+              resolve_stack<typename C::Layout>(a.sp, comp_index(PROJ_DOWN, PART_BIAS, NP), dref))[drow0 + dsub]);
         red_l[r][dsub] = (dw != nullptr) ? sel_sc[r] * p : 0.f;
       }
     }
@@ -1018,9 +1100,9 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
     if (tid < ROWS_D) {
       float yv = 0.f;
       for (int w = 0; w < K; ++w) yv += red_l[w][tid];   // rank order
-      a.y[(size_t)l * D + drow0 + tid] = (uint16_t)f32_to_bf16(yv);
+      KARG(y)[(size_t)l * D + drow0 + tid] = (uint16_t)f32_to_bf16(yv);
     }
-    wg_arrive(counter(a, l, CNT_D));
+    wg_arrive(counter<WS>(a, l, CNT_D));
     if (wave == 0) trace_mark(a, l, TR_D_ARRIVED);
     // ----------------------------- staging loads of layer l+1's prediction
     // (the ranking wave's down rows are staged after the next layer's wait)
@@ -1034,21 +1116,29 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-#define MOE_STACK_GEOM(D, F, K, PB)                                          \
-  {D, F, K, PB,                                                              \
-   (StackCfg<D, F, K, PB>::ITEMS_U > StackCfg<D, F, K, PB>::ITEMS_D          \
-        ? StackCfg<D, F, K, PB>::ITEMS_U                                     \
-        : StackCfg<D, F, K, PB>::ITEMS_D),                                   \
-   reinterpret_cast<const void *>(&stack_decode_kernel<D, F, K, PB>)}
+#define MOE_STACK_GEOM(D, F, K, PB, ACT, MODE, RN)                            \
+  {D, F, K, PB, ACT, MODE, RN,                                               \
+   (StackCfg<D, F, K, PB, ACT, MODE, RN>::ITEMS_U >                          \
+            StackCfg<D, F, K, PB, ACT, MODE, RN>::ITEMS_D                    \
+        ? StackCfg<D, F, K, PB, ACT, MODE, RN>::ITEMS_U                      \
+        : StackCfg<D, F, K, PB, ACT, MODE, RN>::ITEMS_D),                    \
+   StackWs<F, K>::kCnt,                                                      \
+   reinterpret_cast<const void *>(&stack_decode_kernel<D, F, K, PB, ACT, MODE, RN>)}
 
+// Qwen3-30B-A3B: 256 workgroups; softmax top-k with and without renorm
 static const StackLaunch kStackTable[] = {
-    MOE_STACK_GEOM(2048, 768, 8, false),   // Qwen3-30B-A3B: 256 workgroups
+    MOE_STACK_GEOM(2048, 768, 8, false, MOE_ACT_SWIGLU, MOE_ROUTE_SOFTMAX_TOPK, 1),
+    MOE_STACK_GEOM(2048, 768, 8, false, MOE_ACT_SWIGLU, MOE_ROUTE_SOFTMAX_TOPK, 0),
 };
 constexpr int kStackKernels = sizeof(kStackTable) / sizeof(kStackTable[0]);
 
-const StackLaunch *find_stack(int d_model, int d_ff, int k, int has_bias) {
+const StackLaunch *find_stack(int d_model, int d_ff, int k, int has_bias, int act, int mode,
+                              int renorm) {
   for (const auto &e : kStackTable)
-    if (e.d_model == d_model && e.d_ff == d_ff && e.k == k && e.has_bias == (has_bias != 0))
+    if (e.d_model == d_model && e.d_ff == d_ff && e.k == k &&
+        e.has_bias == (has_bias != 0) && e.act == act &&
+        (mode < 0 || (e.mode == mode &&
+                      (mode != MOE_ROUTE_SOFTMAX_TOPK || e.renorm == (renorm != 0)))))
       return &e;
   return nullptr;
 }

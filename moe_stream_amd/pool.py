@@ -79,10 +79,15 @@ class SlotPool:
         self.geom = geom
         self.n_slots = n_slots
         self.device = _norm_device(device)
+        # one array per component, [n_slots, *shape] in its final dtype, all
+        # in one allocation back to back in component order (the layout the
+        # whole-token kernel takes as one base address)
+        self._buf = torch.zeros(n_slots * geom.payload_bytes, dtype=torch.uint8,
+                                device=self.device)
         self.views = {}
         for c in geom.components:
-            self.views[c.name] = torch.zeros((n_slots, *c.shape), dtype=_torch_dtype(c),
-                                             device=self.device)
+            part = self._buf[n_slots * c.offset:n_slots * (c.offset + c.nbytes)]
+            self.views[c.name] = part.view(_torch_dtype(c)).view(n_slots, *c.shape)
         self.pool_bytes = sum(a.numel() * a.element_size() for a in self.views.values())
         self.store = store           # torch uint8 [n_records, record_bytes] or HostStore
         self._view = None

@@ -83,7 +83,8 @@ def _qwen3_view(pad=0, swap_store=False):
     v = _lib.PoolView()
     v.n_components, v.n_slots = len(g.components), 8
     for i, c in enumerate(g.components):
-        v.base[i] = 0x10_0000_0000 + i * 0x1000_0000
+        # the component arrays back to back in one allocation
+        v.base[i] = 0x10_0000_0000 + v.n_slots * c.offset
         v.slot_bytes[i] = c.nbytes + pad
         v.comp_offset[i] = c.offset
     if swap_store:
@@ -114,6 +115,11 @@ def test_persistent_decode_requires_the_packed_pool_layout():
     v.record_bytes += 16384
     assert _stack_call(lib, g, v) == _lib.MOE_ERR_UNSUPPORTED
     assert b"-byte records" in lib.moe_last_error()
+    # per-component arrays that are not one allocation (legal elsewhere)
+    g, v = _qwen3_view()
+    v.base[4] += 4096
+    assert _stack_call(lib, g, v) == _lib.MOE_ERR_UNSUPPORTED
+    assert b"one allocation" in lib.moe_last_error()
     # the packed layout passes this check; the next argument error reports
     g, v = _qwen3_view()
     assert _stack_call(lib, g, v) == _lib.MOE_ERR_INVALID
