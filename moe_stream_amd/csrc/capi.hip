@@ -77,13 +77,6 @@ int check_packed_layout(const moe_pool_view *v, const moe_geom *g) {
       return fail(MOE_ERR_UNSUPPORTED,
                   "persistent decode needs repacked records: component %d at %lld != %lld", c,
                   (long long)v->comp_offset[c], (long long)off);
-    if (v->n_slots > 0 &&
-        static_cast<const char *>(v->base[c]) !=
-            static_cast<const char *>(v->base[0]) + (int64_t)v->n_slots * off)
-      return fail(MOE_ERR_UNSUPPORTED,
-                  "persistent decode needs the pool's component arrays in one allocation, "
-                  "back to back: component %d is not at base[0] + n_slots * %lld", c,
-                  (long long)off);
     off += cb[c];
   }
   const int64_t rec = (off + 16383) / 16384 * 16384;
@@ -430,10 +423,7 @@ int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_lay
     return fail(MOE_ERR_INVALID, "epoch %u too large for %d layers: zero the workspace and "
                 "restart at 1", epoch, n_layers);
   moe::StackArgs a;
-  a.sp.slots = pa.n_slots > 0 ? pa.base[0] : nullptr;
-  a.sp.store = pa.store;
-  a.sp.n_slots = pa.n_slots;
-  a.sp.n_records = pa.n_records;
+  a.pa = pa;
   a.x = x;
   a.W = W;
   a.bias = bias;

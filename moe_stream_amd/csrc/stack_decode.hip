@@ -49,44 +49,8 @@ namespace moe {
 
 constexpr uint32_t kSpinLimit = 1u << 20;
 
-// The pool as this kernel sees it: the packed layout of one geometry with
-// every component array in ONE allocation, back to back in component order
-// (component c's [n_slots, *shape] array at slots + n_slots * offset of c in
-// a record), so one base address stands for all of them; and the store of
-// repacked records.  Few scalar registers: the kernel runs at the limit.
-struct StackPool {
-  const char *slots;
-  const char *store;
-  int32_t n_slots;
-  int32_t n_records;
-};
-
-// resolve() for a StackPool in the packed layout L; nullptr when the
-// reference is out of range.
-template <class L>
-__device__ __forceinline__ const char *resolve_stack(const StackPool &sp, int c, int32_t ref) {
-  if (ref >= 0) {
-    if (ref >= sp.n_slots) return nullptr;
-    return sp.slots + (int64_t)sp.n_slots * L::comp_offset(c) + (int64_t)ref * L::slot_bytes(c);
-  }
-  const int64_t r = -(int64_t)ref - 1;
-  if (sp.store == nullptr || r >= sp.n_records) return nullptr;
-  return sp.store + r * L::kRecordBytes + L::comp_offset(c);
-}
-// As resolve_stack, but an out-of-range reference reads slot 0 (or store
-// record 0 when there are no slots) and clears `ok`.
-template <class L>
-__device__ __forceinline__ const char *resolve_stack_safe(const StackPool &sp, int c,
-                                                          int32_t ref, bool &ok) {
-  const char *p = resolve_stack<L>(sp, c, ref);
-  ok = p != nullptr;
-  return ok ? p
-            : (sp.n_slots > 0 ? sp.slots + (int64_t)sp.n_slots * L::comp_offset(c)
-                              : sp.store + L::comp_offset(c));
-}
-
 struct StackArgs {
-  StackPool sp;
+  PoolArgs pa;
   const uint16_t *x;      // [L][D] bf16 layer inputs
   const uint16_t *W;      // [L][E][D] bf16 routers
   const uint16_t *bias;   // [L][E] bf16 or null
@@ -366,7 +330,7 @@ __device__ __forceinline__ uint32_t u_rows(const StackArgs &a, int32_t ref, int 
   constexpr int SB_U4 = C::SB_U4, NP = C::NP;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int uj = lane % SGU, usub = lane / SGU;
-  const bool ok = resolve_stack<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_W, NP), ref) != nullptr;
+  const bool ok = resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref) != nullptr;
   const int urow = row0 + wave * RPSU + usub;
   float pg = 0.f, pu = 0.f;
   if (ok) {
@@ -391,9 +355,9 @@ __device__ __forceinline__ uint32_t u_rows(const StackArgs &a, int32_t ref, int 
   if (ok) {
     if (C::PBIAS_) {
       pg += bf16_to_f32(reinterpret_cast<const uint16_t *>(
-          resolve_stack<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_BIAS, NP), ref))[urow]);
+          resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref))[urow]);
       pu += bf16_to_f32(reinterpret_cast<const uint16_t *>(
-          resolve_stack<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_BIAS, NP), ref))[urow]);
+          resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref))[urow]);
     }
     hb = f32_to_bf16(stack_act<C>(pg, pu));
   } else if (lane == 0) {
@@ -451,12 +415,12 @@ struct TaskRegs {
     static_assert(C::RPSU == 4 && SGU == 16 && NG * 2 * 4 == 16 * 16,
                   "a task: 4 rows of 16 lanes; its scales: 4 arrays of 16 pieces");
     const int lane = threadIdx.x & 63, uj = lane % SGU, usub = lane / SGU;
-    const char *gw = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
-    const char *uw = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_W, NP), ref, ok);
-    const char *gs = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_S, NP), ref, ok);
-    const char *gb = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_B, NP), ref, ok);
-    const char *us = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_S, NP), ref, ok);
-    const char *ub = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_B, NP), ref, ok);
+    const char *gw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
+    const char *uw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
+    const char *gs = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok);
+    const char *gb = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok);
+    const char *us = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok);
+    const char *ub = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok);
     const int arr = lane >> 4, row = 4 * b + usub;
     const char *sa = arr == 0 ? gs : arr == 1 ? gb : arr == 2 ? us : ub;
     sv = load16(reinterpret_cast<const uint4 *>(sa + (int64_t)(4 * b) * NG * 2) + (lane & 15));
@@ -464,9 +428,9 @@ struct TaskRegs {
     if (C::PBIAS_) {
       bool okb;
       gbv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-          resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[row]);
+          resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[row]);
       ubv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-          resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[row]);
+          resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[row]);
     }
     issue_order_fence();
     const uint4 *g4 = reinterpret_cast<const uint4 *>(gw + (int64_t)row * (D / 2)) + uj;
@@ -507,12 +471,12 @@ __device__ __forceinline__ bool task_stage_lds(const StackArgs &a, int32_t ref, 
   typedef __attribute__((address_space(3))) void lds_void;
   const int lane = threadIdx.x & 63, uj = lane % SGU, usub = lane / SGU;
   bool ok;
-  const char *gw = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
-  const char *uw = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_W, NP), ref, ok);
-  const char *gs = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_S, NP), ref, ok);
-  const char *gb = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_B, NP), ref, ok);
-  const char *us = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_S, NP), ref, ok);
-  const char *ub = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_B, NP), ref, ok);
+  const char *gw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
+  const char *uw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
+  const char *gs = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok);
+  const char *gb = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok);
+  const char *us = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok);
+  const char *ub = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok);
   const int arr = lane >> 4, row = 4 * b + usub;
   const char *sa = arr == 0 ? gs : arr == 1 ? gb : arr == 2 ? us : ub;
   const uint4 *g4 = reinterpret_cast<const uint4 *>(gw + (int64_t)row * (D / 2)) + uj;
@@ -562,9 +526,9 @@ __device__ __forceinline__ uint32_t task_rows_lds(const StackArgs &a, int32_t re
   if (C::PBIAS_) {
     bool okb;
     gbv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-        resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[4 * b + usub]);
+        resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[4 * b + usub]);
     ubv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-        resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[4 * b + usub]);
+        resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[4 * b + usub]);
   }
   uint4 cg[CPLU], cu[CPLU];
 #pragma unroll
@@ -630,12 +594,12 @@ __device__ __forceinline__ void u_load(const StackArgs &a, int32_t ref, int row0
   // clamped index.
   ref = __builtin_amdgcn_readfirstlane(ref);
   bool ok;
-  const char *gw = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
-  const char *uw = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_W, NP), ref, ok);
-  const char *sb[4] = {resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_S, NP), ref, ok),
-                       resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_GATE, PART_B, NP), ref, ok),
-                       resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_S, NP), ref, ok),
-                       resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_UP, PART_B, NP), ref, ok)};
+  const char *gw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
+  const char *uw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
+  const char *sb[4] = {resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok),
+                       resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok),
+                       resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok),
+                       resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok)};
 #pragma unroll
   for (int it = 0; it < C::SIT; ++it) {
     const int i = min(it * NT + tid, 4 * SB_U4 - 1);
@@ -666,9 +630,9 @@ __device__ __forceinline__ void d_load(const StackArgs &a, int32_t ref, int drow
   // (unconditional loads, as in u_load)
   ref = __builtin_amdgcn_readfirstlane(ref);
   bool ok;
-  const char *dw = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_DOWN, PART_W, NP), ref, ok);
-  const char *ds = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_DOWN, PART_S, NP), ref, ok);
-  const char *db = resolve_stack_safe<typename C::Layout>(a.sp, comp_index(PROJ_DOWN, PART_B, NP), ref, ok);
+  const char *dw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_W, NP), ref, ok);
+  const char *ds = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_S, NP), ref, ok);
+  const char *db = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_B, NP), ref, ok);
 #pragma unroll
   for (int it = 0; it < C::SDIT; ++it) {
     const int i = min(it * 64 + lane, 2 * SBD_U4 - 1);
@@ -1037,7 +1001,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
     if (wave < K) {
       const int r = d_r, fx = d_fx;
       const int32_t dref = d_ref;
-      const char *dw = resolve_stack<typename C::Layout>(a.sp, comp_index(PROJ_DOWN, PART_W, NP), dref);
+      const char *dw = resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_W, NP), dref);
 
       uint4 *hact = hact_l[wave];
       float *hsum = hsum_l[wave];
@@ -1092,7 +1056,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       if (dj == 0) {
         if (PBIAS && dw != nullptr)
           p += bf16_to_f32(reinterpret_cast<const uint16_t *>(
-              resolve_stack<typename C::Layout>(a.sp, comp_index(PROJ_DOWN, PART_BIAS, NP), dref))[drow0 + dsub]);
+              resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_BIAS, NP), dref))[drow0 + dsub]);
         red_l[r][dsub] = (dw != nullptr) ? sel_sc[r] * p : 0.f;
       }
     }

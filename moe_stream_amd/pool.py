@@ -80,8 +80,7 @@ class SlotPool:
         self.n_slots = n_slots
         self.device = _norm_device(device)
         # one array per component, [n_slots, *shape] in its final dtype, all
-        # in one allocation back to back in component order (the layout the
-        # whole-token kernel takes as one base address)
+        # in one allocation back to back in component order
         self._buf = torch.zeros(n_slots * geom.payload_bytes, dtype=torch.uint8,
                                 device=self.device)
         self.views = {}
