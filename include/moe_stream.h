@@ -113,6 +113,24 @@ int moe_ffn_decode(const moe_pool_view *pool, const moe_geom *g,
                    uint16_t *out_bf16, float *out_f32,
                    void *workspace, size_t workspace_bytes, void *stream);
 
+/*
+ * moe_ffn_decode for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
+ * no workspace argument, nothing allocated or freed.  This entry point has
+ * no counterpart in the reference.  The [T*k, d_ff] activations go to a
+ * fixed device array of the library, one per GPU, held until the process
+ * ends: T * k * d_ff * 2 bytes must not exceed moe_ffn_decode_static_bytes()
+ * (2 MiB; MOE_ERR_INVALID beyond, before any device work).  Every call on a
+ * GPU shares that GPU's array, so calls that overlap on one GPU (other
+ * streams, other threads) race; calls ordered on one stream do not.
+ * Results are those of moe_ffn_decode (the same kernels).
+ */
+size_t moe_ffn_decode_static_bytes(void);
+int moe_ffn_decode_static(const moe_pool_view *pool, const moe_geom *g,
+                          const int32_t *slot_refs, const float *scores,
+                          const uint16_t *x, int32_t T, int32_t k,
+                          uint16_t *out_bf16, float *out_f32, void *stream);
+
 /* The two halves of moe_ffn_decode, for callers that time or schedule them
  * separately: _up writes the bf16 [T*k, d_ff] activations into the
  * workspace, _down reads them (same workspace) and writes the combined

@@ -36,6 +36,7 @@ EXPORTS = (
     "moe_version", "moe_last_error", "moe_component_bytes",
     "moe_ffn_decode_workspace", "moe_ffn_decode",
     "moe_ffn_decode_up", "moe_ffn_decode_down",
+    "moe_ffn_decode_static_bytes", "moe_ffn_decode_static",
     "moe_ffn_grouped_workspace", "moe_ffn_grouped",
     "moe_route_workspace", "moe_route", "moe_slot_lookup",
     "moe_stack_workspace", "moe_stack_decode", "moe_stack_trace",
@@ -88,6 +89,9 @@ def _declare(lib):
         "moe_ffn_decode_workspace": (SZ, [C.POINTER(Geom), I32, I32]),
         "moe_ffn_decode": (C.c_int, [C.POINTER(PoolView), C.POINTER(Geom), P, P, P,
                                      I32, I32, P, P, P, SZ, P]),
+        "moe_ffn_decode_static_bytes": (SZ, []),
+        "moe_ffn_decode_static": (C.c_int, [C.POINTER(PoolView), C.POINTER(Geom), P, P, P,
+                                            I32, I32, P, P, P]),
         "moe_ffn_decode_up": (C.c_int, [C.POINTER(PoolView), C.POINTER(Geom), P, P,
                                         I32, I32, P, SZ, P]),
         "moe_ffn_decode_down": (C.c_int, [C.POINTER(PoolView), C.POINTER(Geom), P, P,

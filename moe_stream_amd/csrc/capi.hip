@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "launchers.h"
@@ -243,6 +244,75 @@ int moe_ffn_decode(const moe_pool_view *pool, const moe_geom *g,
                          static_cast<uint16_t *>(workspace), out_bf16, out_f32,
                          g->act, g->alpha, g->limit,
                          static_cast<hipStream_t>(stream));
+  MOE_HIP(hipGetLastError());
+  return MOE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// moe_ffn_decode without a caller workspace: the [T*k, d_ff] activations go
+// to `scratch`, a fixed device array of this library (one per GPU, held
+// until the process ends).  Its device address is looked up once per device
+// on the first call there, with that device current; host code uses only
+// that address (the array's name is a host-side stand-in).
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr size_t kScratchBytes = (size_t)2 << 20;   // MOE_FFN_DECODE_STATIC_BYTES
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void *g_scratch_ptr[kScratchDevices] = {};
+
+// The current device's scratch address, looked up on its first use.
+static int scratch_ptr(void **out) {
+  int dev = 0;
+  MOE_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kScratchDevices)
+    return fail(MOE_ERR_UNSUPPORTED, "device %d beyond the %d the static scratch serves", dev,
+                kScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    MOE_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(MOE_ERR_HIP, "hipGetSymbolAddress(scratch) gave NULL");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MOE_OK;
+}
+
+}  // namespace
+
+size_t moe_ffn_decode_static_bytes(void) { return kScratchBytes; }
+
+int moe_ffn_decode_static(const moe_pool_view *pool, const moe_geom *g,
+                          const int32_t *slot_refs, const float *scores,
+                          const uint16_t *x, int32_t T, int32_t k, uint16_t *out_bf16,
+                          float *out_f32, void *stream) {
+  if (!g) return fail(MOE_ERR_INVALID, "geom is NULL");
+  if (T <= 0 || k <= 0) return fail(MOE_ERR_INVALID, "T=%d k=%d must be positive", T, k);
+  const size_t need = moe_ffn_decode_workspace(g, T, k);
+  if (need > kScratchBytes)
+    return fail(MOE_ERR_INVALID,
+                "T=%d x k=%d x d_ff=%d activations need %zu bytes, above the %zu-byte "
+                "static scratch: call moe_ffn_decode with a workspace", T, k, g->d_ff, need,
+                kScratchBytes);
+  moe::PoolArgs pa;
+  const moe::FfnLaunch *L = nullptr;
+  // the size checks above come first, so an oversized call does no device work
+  void *ws = nullptr;
+  int rc = scratch_ptr(&ws);
+  if (rc) return rc;
+  rc = ffn_prepare(pool, g, slot_refs, T, k, ws, kScratchBytes, &pa, &L);
+  if (rc) return rc;
+  if (!scores || !x) return fail(MOE_ERR_INVALID, "NULL scores/x");
+  if (!out_bf16 && !out_f32) return fail(MOE_ERR_INVALID, "no output buffer");
+  if (!aligned(x, 16)) return fail(MOE_ERR_INVALID, "x must be 16-byte aligned");
+  (void)hipGetLastError();
+  moe::launch_ffn_decode(L, pa, device_refs(slot_refs), scores, x, T, k,
+                         static_cast<uint16_t *>(ws), out_bf16, out_f32, g->act, g->alpha,
+                         g->limit, static_cast<hipStream_t>(stream));
   MOE_HIP(hipGetLastError());
   return MOE_OK;
 }

@@ -175,3 +175,14 @@ def test_fill_slots_range_checks_records_and_slots():
     assert b"slot 8 outside [0, 8)" in lib.moe_last_error()
     assert lib.moe_fill_slots(C.byref(v), src, rb, 0, recs, slots, 2, None) == \
         _lib.MOE_ERR_INVALID
+
+
+def test_static_scratch_decode_rejects_oversized_calls_first():
+    """The no-allocation decode checks the activation size against its fixed
+    scratch before any device call."""
+    lib = _lib.lib()
+    assert lib.moe_ffn_decode_static_bytes() == 2 << 20
+    g = G.QWEN3_30B_A3B.c_geom()
+    T = (2 << 20) // (8 * 768 * 2) + 1
+    rc = lib.moe_ffn_decode_static(None, C.byref(g), None, None, None, T, 8, None, None, None)
+    assert rc == _lib.MOE_ERR_INVALID and b"static scratch" in lib.moe_last_error()
