@@ -34,9 +34,12 @@ def parse():
     ap.add_argument("--tokens", type=int, default=64)
     ap.add_argument("--workload", default="qwen3-48l",
                     choices=["qwen3-48l", "gptoss-36l", "qwen3-prefill", "qwen3-stream",
-                             "hbm-copy"],
+                             "qwen3-verify", "hbm-copy"],
                     help="qwen3-prefill: 512 tokens per layer through the grouped "
-                         "MFMA path; qwen3-stream: 256 decode tokens over a 2048-slot "
+                         "MFMA path; qwen3-verify: 8 tokens per layer (a speculative "
+                         "verification step) through the small-T grouped decode block, "
+                         "against the same tokens decoded one at a time; "
+                         "qwen3-stream: 256 decode tokens over a 2048-slot "
                          "pool fed from a pinned host store; hbm-copy: a 1 GiB device "
                          "copy, the achievable HBM rate and the known-size reference "
                          "for the FETCH_SIZE / WRITE_SIZE counters (secondary "
@@ -183,6 +186,70 @@ def prefill(args):
                         "avg_block_us": round(float(block_ms.mean()) * 1e3, 2)},
            "expert_weight_GBs": round(wbytes / block_s / 1e9, 1),
            "wall_s": round(wall, 3)}
+    print(json.dumps(out), flush=True)
+
+
+def verify(args):
+    """A speculative verification step (gamma + 1 = 8 draft tokens, the
+    multi-token call of spec.py:192-194) on the 48-layer Qwen3 stack: per
+    layer the router for the 8 tokens and the small-T grouped expert block
+    (each distinct expert's weights read once for every token routed to it),
+    the 48 layers captured as one HIP graph.  Interleaved in the same run:
+    the same 8 tokens decoded one at a time by the whole-token kernel.  One
+    step = one verification; value = verified tokens per second."""
+    import torch
+    from moe_stream_amd import geometry as G
+    from moe_stream_amd import ops, synth
+    from moe_stream_amd.stack import PrefillStack
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    T = args.tokens if args.tokens != 64 else 8
+    L, slots, geom = 48, 3072, G.QWEN3_30B_A3B
+    stack = PrefillStack(geom, L, slots, T, dev, block="decode", zipf_s=1.1)
+    n_steps = args.warmup + args.steps
+    xs = synth.hidden_states(T * n_steps, L, geom.d_model, dev, synth.SEED_BASE + 500)
+    xs = xs.view(n_steps, T, L, geom.d_model)
+    stack.x_in.copy_(xs[0].transpose(0, 1))
+    stack.capture()
+    s = torch.cuda.current_stream()
+    ver_ms, seq_ms, distinct = [], [], []
+    for i in range(n_steps):
+        x_step = xs[i].transpose(0, 1).contiguous()          # [L, T, D]
+        a, b, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        stack.x_in.copy_(x_step)
+        a.record(s)
+        stack.graph.replay()
+        b.record(s)
+        for t in range(T):                                   # one token at a time
+            stack.token_persistent(xs[i, t], ordinary=True)
+        c.record(s)
+        c.synchronize()
+        if i >= args.warmup:
+            ver_ms.append(a.elapsed_time(b))
+            seq_ms.append(b.elapsed_time(c))
+            distinct.append(int((stack.routed_counts() > 0).sum()))
+    stack.check_persistent()
+    ops.check_device_error()
+    ver, seq = float(np.median(ver_ms)), float(np.median(seq_ms))
+    wbytes = float(np.mean(distinct)) * geom.payload_bytes
+    out = {"metric": "MoE speculative verification tok/s (8 tokens x 48 layers, small-T "
+                     "grouped decode block)",
+           "value": round(T / (ver / 1e3), 1), "unit": "tok/s", "n_gpus": 1,
+           "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ver, 4),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "bf16", "data": "synthetic",
+           "config": {"workload": "qwen3-30b-a3b-moe-stack-verify", "layers": L,
+                      "tokens_per_step": T, "top_k": stack.k, "pool_slots": slots,
+                      "router_bias": "zipf(1.1) log-popularity",
+                      "launch": "one HIP graph per step: route + 2 grouped decode kernels "
+                                "per layer", "parallelism": "none (1 GPU)"},
+           "ms_per_verify": round(ver, 4),
+           "ms_same_tokens_one_at_a_time": round(seq, 4),
+           "speedup_vs_one_at_a_time": round(seq / ver, 3),
+           "pairs_per_layer": T * stack.k,
+           "distinct_experts_per_layer": round(float(np.mean(distinct)) / L, 2),
+           "expert_bytes_per_verify": int(wbytes),
+           "expert_GBs": round(wbytes / (ver * 1e-3) / 1e9, 1)}
     print(json.dumps(out), flush=True)
 
 
@@ -423,6 +490,8 @@ def main():
         return stream(args)
     if args.workload == "hbm-copy":
         return hbm_copy(args)
+    if args.workload == "qwen3-verify":
+        return verify(args)
     import torch
     from moe_stream_amd import synth
     dev = torch.device("cuda:0")

@@ -6,15 +6,25 @@
 namespace moe {
 
 // ---- batch-1 / small-T expert block (ffn_decode.hip) ----------------------
+// Small-T grouped kernels: up to this many (token, expert) pairs per call,
+// member tokens of a slot staged this many at a time.
+constexpr int kSmallMaxPairs = 256;
+constexpr int kSmallTokensPerPass = 8;
 struct FfnLaunch {
   int d_model, d_ff, has_bias;
   int up_rows_wg, up_threads;  // gate/up kernel: rows and threads per WG
   int down_rows_wg;            // down kernel: output rows per WG
+  int down_small_waves;        // grouped down kernel: waves per WG
   void (*up)(dim3, dim3, hipStream_t, const PoolArgs &, const RefList &,
              const uint16_t *, int, uint16_t *, int, float, float);
   void (*down)(dim3, dim3, hipStream_t, const PoolArgs &, const RefList &,
                const float *, const uint16_t *, int, uint16_t *, float *);
   size_t (*down_lds)(int k);   // dynamic LDS bytes of the down kernel
+  void (*up_small)(dim3, dim3, hipStream_t, const PoolArgs &, const int32_t *, int,
+                   const uint16_t *, int, uint16_t *, int, float, float);
+  void (*down_small)(dim3, dim3, size_t, hipStream_t, const PoolArgs &, const int32_t *,
+                     const float *, const uint16_t *, int, int, uint16_t *, float *);
+  size_t (*down_small_lds)(int P);   // dynamic LDS bytes of the grouped down kernel
 };
 const FfnLaunch *find_ffn(int d_model, int d_ff, int has_bias);
 void launch_ffn_up(const FfnLaunch *L, const PoolArgs &pa, const RefList &refs,

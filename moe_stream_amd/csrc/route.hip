@@ -24,6 +24,8 @@
 // engine_120b.py:73-75), slot lookup (engine_v3.py:548-552).  Ranking is
 // value-descending with ties to the lower expert id (argpartition leaves the
 // order of ties unspecified).
+#include <algorithm>
+
 #include "launchers.h"
 
 namespace moe {
@@ -165,14 +167,21 @@ __device__ __forceinline__ void router_rows(const RouteArgs &a, int row, int lan
     const int i = lane + it * 64;
     w[it] = (i < n8) ? load_stream16(w4 + i) : make_uint4(0, 0, 0, 0);
   }
+  // the next token's activations load while this one's dot product runs
+  uint4 vn[NIT];
+  auto load_x = [&](int t) {
+    const uint4 *x4 = reinterpret_cast<const uint4 *>(a.x + (int64_t)min(t, a.T - 1) * a.D);
+#pragma unroll
+    for (int it = 0; it < NIT; ++it)
+      vn[it] = x4[min(lane + it * 64, n8 - 1)];   // unconditional, masked below
+  };
+  load_x(0);
   for (int t = 0; t < a.T; ++t) {
-    const uint4 *x4 = reinterpret_cast<const uint4 *>(a.x + (int64_t)t * a.D);
     uint4 v[NIT];
 #pragma unroll
-    for (int it = 0; it < NIT; ++it) {
-      const int i = lane + it * 64;
-      v[it] = (i < n8) ? x4[i] : make_uint4(0, 0, 0, 0);
-    }
+    for (int it = 0; it < NIT; ++it)
+      v[it] = (lane + it * 64 < n8) ? vn[it] : make_uint4(0, 0, 0, 0);
+    load_x(t + 1);
     float acc = 0.f;
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
@@ -223,13 +232,14 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   const int nrows = a.E * (a.Wn ? 2 : 1);
   const int row = blockIdx.x * 4 + wave;
   if (row < nrows) router_rows<NIT>(a, row, lane, fl);
-  if (blockIdx.x != 0) return;
 
-  // ---- workgroup 0 ranks: one wave per (token, router|lookahead) task ----
-  // The logits travel as flagged device-scope (sc1) entries, coherent across
-  // XCDs without L2 writeback/invalidate; the poll of an entry is its load.
+  // ---- ranking: one wave per (token, router|lookahead) task, on the first
+  // workgroups.  The logits travel as flagged device-scope (sc1) entries,
+  // coherent across XCDs without L2 writeback/invalidate; the poll of an
+  // entry is its load.
   const int ntask = a.T * (a.Wn ? 2 : 1);
-  for (int task = wave; task < ntask; task += 4) {
+  const int task = blockIdx.x * 4 + wave;
+  if (task < ntask) {
     const TaskPre p = task_pre(a, task, lane);
     const bool la = task >= a.T;
     float l0, l1;
@@ -237,6 +247,11 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
                 l0, l1);
     select_task(a, task, lane, p, l0, l1);
   }
+  // Workgroup 0 advances the sequence word once its task 0 has seen all of
+  // token 0's router entries: every row writer read the word before writing
+  // them, so no writer of this launch can read the advanced value, and the
+  // other ranking waves polled with the same flag.
+  if (blockIdx.x != 0) return;
   __syncthreads();
   if (threadIdx.x == 0)
     __hip_atomic_store(a.counter, fl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -335,8 +350,9 @@ void launch_route(const RouteArgs &a, hipStream_t s) {
     return;
   }
   const int nrows = a.E * (a.Wn ? 2 : 1);
+  const int ntask = a.T * (a.Wn ? 2 : 1);
   const int nit = (a.D / 8 + 63) / 64;
-  dim3 g((nrows + 3) / 4), b(256);
+  dim3 g((std::max(nrows, ntask) + 3) / 4), b(256);
   switch (nit) {
     case 1: hipLaunchKernelGGL(route_kernel<1>, g, b, 0, s, a); break;
     case 2: hipLaunchKernelGGL(route_kernel<2>, g, b, 0, s, a); break;

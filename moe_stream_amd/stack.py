@@ -249,19 +249,23 @@ class PrefillStack(DecodeStack):
     those of DecodeStack."""
 
     def __init__(self, geom: Geometry, n_layers: int, n_slots: int, n_tokens: int,
-                 device="cuda", **kw):
+                 device="cuda", block: str = "grouped", **kw):
+        """block: "grouped" -- the MFMA block for many tokens (prefill);
+        "decode" -- the decode kernels, whose small-T form groups the pairs by
+        slot (a multi-token verification step of a few tokens)."""
         super().__init__(geom, n_layers, n_slots, device, **kw)
         import ctypes as C
         self.T = n_tokens
+        self.block = block
         dev = self.device
         self.bufs = [ops.RouteBuffers(n_tokens, self.k, self.k_pred, dev)
                      for _ in range(n_layers)]
         self.route_ws = torch.zeros(_lib.lib().moe_route_workspace(n_tokens, self.E),
                                     dtype=torch.uint8, device=dev)
         g = geom.c_geom()
-        self.ffn_ws = torch.zeros(
-            _lib.lib().moe_ffn_grouped_workspace(C.byref(g), n_tokens, self.k),
-            dtype=torch.uint8, device=dev)
+        ws = (_lib.lib().moe_ffn_grouped_workspace if block == "grouped"
+              else _lib.lib().moe_ffn_decode_workspace)(C.byref(g), n_tokens, self.k)
+        self.ffn_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)
         self.x_in = torch.zeros((n_layers, n_tokens, geom.d_model), dtype=torch.bfloat16,
                                 device=dev)
         self.y = torch.zeros((n_layers, n_tokens, geom.d_model), dtype=torch.bfloat16,
@@ -277,8 +281,9 @@ class PrefillStack(DecodeStack):
                   W_next=self.W[Lx + 1] if nxt else None, bias_next=bn,
                   k_pred=self.k_pred, table=self.table[Lx], bufs=bufs,
                   stream=stream, workspace=self.route_ws)
-        ops.ffn_grouped(self.pool, bufs.slot_refs, bufs.scores, self.x_in[Lx],
-                        out=self.y[Lx], stream=stream, workspace=self.ffn_ws)
+        f = ops.ffn_grouped if self.block == "grouped" else ops.ffn_decode
+        f(self.pool, bufs.slot_refs, bufs.scores, self.x_in[Lx], out=self.y[Lx],
+          stream=stream, workspace=self.ffn_ws)
 
     def run_step(self, x_step: torch.Tensor, use_graph: bool = True):
         """x_step: bf16 [n_layers, T, d_model], the residual stream of T tokens
