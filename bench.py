@@ -44,8 +44,9 @@ def parse():
                          "copy, the achievable HBM rate and the known-size reference "
                          "for the FETCH_SIZE / WRITE_SIZE counters (secondary "
                          "measurements, not the headline)")
-    ap.add_argument("--mode", default="persistent", choices=["persistent", "graph", "eager"],
-                    help="persistent: one launch per token; graph/eager: 3 launches per layer")
+    ap.add_argument("--mode", default="auto", choices=["auto", "persistent", "graph", "eager"],
+                    help="persistent: one launch per token; graph/eager: 3 launches per layer; "
+                         "auto: the faster of the two for the geometry")
     ap.add_argument("--launch", default="ordinary", choices=["ordinary", "cooperative"],
                     help="persistent mode: the bench owns the GPU, so an ordinary launch "
                          "(checked after the timed steps; if a launch timed out the steps "
@@ -500,6 +501,8 @@ def main():
     xs = synth.hidden_states(args.tokens, stack.L, stack.geom.d_model, dev,
                              synth.SEED_BASE + 200)
     mode = args.mode
+    if mode == "auto":
+        mode = "persistent" if stack.persistent_preferred() else "graph"
     if mode == "persistent" and not stack.persistent_supported():
         mode = "graph"
     if mode == "graph":

@@ -1079,6 +1079,12 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
   }
 }
 
+}  // namespace moe
+
+#include "stack_wide.hip"
+
+namespace moe {
+
 // ---------------------------------------------------------------------------
 #define MOE_STACK_GEOM(D, F, K, PB, ACT, MODE, RN)                            \
   {D, F, K, PB, ACT, MODE, RN,                                               \
@@ -1090,9 +1096,16 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
    reinterpret_cast<const void *>(&stack_decode_kernel<D, F, K, PB, ACT, MODE, RN>)}
 
 // Qwen3-30B-A3B: 256 workgroups; softmax top-k with and without renorm
+#define MOE_STACK_WIDE(D, F, K, PB, ACT, MODE, RN)                            \
+  {D, F, K, PB, ACT, MODE, RN, WideCfg<D, F, K, PB, ACT, MODE, RN>::NWG,     \
+   StackWs<F, K>::kCnt,                                                      \
+   reinterpret_cast<const void *>(&stack_wide_kernel<D, F, K, PB, ACT, MODE, RN>)}
+
 static const StackLaunch kStackTable[] = {
     MOE_STACK_GEOM(2048, 768, 8, false, MOE_ACT_SWIGLU, MOE_ROUTE_SOFTMAX_TOPK, 1),
     MOE_STACK_GEOM(2048, 768, 8, false, MOE_ACT_SWIGLU, MOE_ROUTE_SOFTMAX_TOPK, 0),
+    // gpt-oss-120b: 256 workgroups (240 with gate/up rows, 180 with down rows)
+    MOE_STACK_WIDE(2880, 2880, 4, true, MOE_ACT_SWIGLU_CLAMP, MOE_ROUTE_TOPK_SOFTMAX, 0),
 };
 constexpr int kStackKernels = sizeof(kStackTable) / sizeof(kStackTable[0]);
 

@@ -132,13 +132,27 @@ class DecodeStack:
             self.token_eager()
 
     # -- one launch per token ---------------------------------------------
+    # geometries and routing rules with a whole-token kernel: (d_model, d_ff,
+    # top-k, projection bias, activation, routing)
+    PERSISTENT = {(2048, 768, 8, False, _lib.MOE_ACT_SWIGLU, _lib.MOE_ROUTE_SOFTMAX_TOPK),
+                  (2880, 2880, 4, True, _lib.MOE_ACT_SWIGLU_CLAMP, _lib.MOE_ROUTE_TOPK_SOFTMAX)}
+
+    # geometries whose whole-token kernel is the faster decode: the gpt-oss
+    # kernel is bit-exact but measured below the per-layer graph replay
+    # (about 1000 vs 1140 tokens/s over 36 layers on one MI355X)
+    PERSISTENT_PREFERRED = {(2048, 768, 8, False, _lib.MOE_ACT_SWIGLU, _lib.MOE_ROUTE_SOFTMAX_TOPK)}
+
+    def persistent_preferred(self) -> bool:
+        g = self.geom
+        return self.persistent_supported() and \
+            (g.d_model, g.d_ff, self.k, g.has_proj_bias, g.act, g.routing) in self.PERSISTENT_PREFERRED
+
     def persistent_supported(self) -> bool:
         import ctypes as C
         L = _lib.lib()
-        g = self.geom.c_geom()
-        return L.moe_stack_workspace(C.byref(g), self.L, self.E, self.k) > 0 and \
-            (self.geom.d_model, self.geom.d_ff, self.k, self.geom.has_proj_bias) in \
-            {(2048, 768, 8, False)}
+        g = self.geom
+        return L.moe_stack_workspace(C.byref(g.c_geom()), self.L, self.E, self.k) > 0 and \
+            (g.d_model, g.d_ff, self.k, g.has_proj_bias, g.act, g.routing) in self.PERSISTENT
 
     # the launch count after which the persistent workspace is zeroed and the
     # epoch restarts at 1 (the kernel's per-layer flags, epoch * n_layers + l,

@@ -82,3 +82,35 @@ def test_persistent_layer_against_oracle(stack):
             zn = N.router_logits(x64, Wb[l + 1], bb[l + 1], "mlx")
             want = N.top_k_indices(zn, stack.k_pred)
             assert N.ids_match(zn, want, stack.p_pred[l].cpu().numpy())
+
+
+@pytest.fixture(scope="module")
+def gptoss_stack():
+    geom = G.GPT_OSS_120B
+    # 4 layers, 240 slots (under half the pairs): refs of both signs
+    st = DecodeStack(geom, 4, 240, "cuda", seed=20260621, zipf_s=None, router_bias=True)
+    yield st
+    del st
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("ordinary", [False, True])
+def test_gptoss_persistent_equals_per_layer(gptoss_stack, ordinary):
+    """The wide whole-token kernel (gpt-oss geometry: top-4 of raw logits,
+    projection biases, clamped SwiGLU) against the per-layer launches:
+    routing, lookahead and outputs bit for bit over several tokens, with
+    mispredicted experts (fix-ups) and store-resident experts."""
+    st = gptoss_stack
+    assert st.persistent_supported()
+    xs = synth.hidden_states(5, st.L, 2880, "cuda", 20260622 + int(ordinary))
+    for t in range(xs.shape[0]):
+        st.run_token(xs[t], use_graph=False)
+        ids, sc, refs, pred = st.routed()
+        y_ref = st.y.clone()
+        st.token_persistent(xs[t], ordinary=ordinary)
+        st.check_persistent()
+        np.testing.assert_array_equal(st.p_ids.cpu().numpy(), ids)
+        np.testing.assert_array_equal(st.p_scores.cpu().numpy(), sc)
+        np.testing.assert_array_equal(st.p_refs.cpu().numpy(), refs)
+        np.testing.assert_array_equal(st.p_pred.cpu().numpy()[:-1], pred[:-1])
+        assert torch.equal(st.p_y, y_ref), t
