@@ -855,7 +855,8 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
         }
         if (lane == 0) {
           pred_cnt[(l + 1) & 1] = min(a.kp, K);
-          spare_cnt[(l + 1) & 1] = max(0, ksel - K);
+          spare_cnt[(l + 1) & 1] = min(kSpare, max(0, ksel - K));   // a wider k_pred: ranks
+                                                                     // past K + kSpare unused
         }
       }
     } else {

@@ -41,6 +41,30 @@ def test_persistent_equals_per_layer(stack):
     assert int(stack.p_miss.sum()) > 0          # some experts read from the store
 
 
+def test_persistent_wide_lookahead_equals_per_layer():
+    """k_pred = 16 (twice top-k): the lookahead ranks 16 experts, of which
+    the kernel stages K and speculates on its spare positions only; every
+    output equals the per-layer launches' (a wider k_pred once let spare
+    tasks past the spare positions write into the fix-up entries)."""
+    st = DecodeStack(G.QWEN3_30B_A3B, 4, 256, "cuda", seed=20260611, zipf_s=1.1, widen=2)
+    assert st.k_pred == 16
+    xs = synth.hidden_states(4, st.L, 2048, "cuda", 20260612)
+    for t in range(xs.shape[0]):
+        st.run_token(xs[t], use_graph=False)
+        ids, sc, refs, pred = st.routed()
+        y_ref = st.y.clone()
+        st.token_persistent(xs[t])
+        torch.cuda.synchronize()
+        ops.check_device_error()
+        np.testing.assert_array_equal(st.p_ids.cpu().numpy(), ids)
+        np.testing.assert_array_equal(st.p_scores.cpu().numpy(), sc)
+        np.testing.assert_array_equal(st.p_refs.cpu().numpy(), refs)
+        np.testing.assert_array_equal(st.p_pred.cpu().numpy()[:-1], pred[:-1])
+        assert torch.equal(st.p_y, y_ref), t
+    del st
+    torch.cuda.empty_cache()
+
+
 def test_graph_replays_equal_eager(stack):
     """The per-layer launches captured once as a HIP graph and replayed for
     several tokens, with eager work of the same stack between the replays:
