@@ -5,8 +5,8 @@
 //   group_pairs_kernel : counting sort of the pairs by slot reference, one
 //                        workgroup; emits perm (sorted row -> pair) and the
 //                        list of 64-row tiles {ref, first row, rows}
-//   grouped_gate_up    : per (tile, 64 features): H = act(X Wg^T, X Wu^T)
-//   grouped_down       : per (tile, 64 outputs):  Yp[pair] = score * H Wd^T
+//   grouped_mm (gate/up): per (tile, NB features): H = act(X Wg^T, X Wu^T)
+//   grouped_mm (down)   : per (tile, NB outputs):  Yp[pair] = score * H Wd^T
 //   combine_pairs      : y[t] = sum over ranks r of Yp[t*k + r] (rank order)
 //
 // Dequantisation rides on the MFMA.  A word of eight 4-bit codes becomes a
@@ -25,6 +25,7 @@
 // (token, rank) (engine_v3.py:588-598, engine_120b.py:132-143) and the
 // score-weighted sum over ranks (engine_v3.py:600, engine_120b.py:145).
 #include <algorithm>
+#include <type_traits>
 
 #include "launchers.h"
 
@@ -40,26 +41,7 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(uint4 a, uint4 b, f32x4_t c) {
 }
 
 constexpr int kTileM = 64;
-
-// The bias term of one LDS pass, sum over its groups g of rowsum[row][g] *
-// C[g][n], as fp32 MFMAs of K = 4 groups: A = the row sums (lane: row l%16,
-// group l/16 of the 4-group chunk), B = this lane's feature's C of group
-// l/16 of the chunk, accumulated straight into the output tile (the layout
-// of the 16x16x32 products).  Replaces one FMA per output element and group.
-template <int GPS>
-__device__ __forceinline__ void bias_term(const float *rs_l, const float (&C)[GPS], int mb,
-                                          int col, int kq, f32x4_t &o) {
-#pragma unroll
-  for (int c = 0; c < (GPS + 3) / 4; ++c) {
-    float cb = 0.f;
-#pragma unroll
-    for (int g = 4 * c; g < (GPS < 4 * c + 4 ? GPS : 4 * c + 4); ++g)
-      if (kq == g - 4 * c) cb = C[g];
-    const int kk = 4 * c + kq;
-    const float ra = rs_l[(kk < GPS ? kk : GPS - 1) * kTileM + mb * 16 + col];
-    o = __builtin_amdgcn_mfma_f32_16x16x4f32(kk < GPS ? ra : 0.f, cb, o, 0, 0, 0);
-  }
-}
+constexpr int kRsPitch = 80;   // row-sum LDS pitch (floats): 4 groups' rows on distinct banks
 
 // ---------------------------------------------------------------------------
 // grouping: one workgroup of 1024 threads; hist[] in dynamic LDS spans every
@@ -129,11 +111,6 @@ __global__ __launch_bounds__(1024) void group_pairs_kernel(
   }
 }
 
-// Groups of 64 inputs staged per LDS pass: a divisor of the group count.
-constexpr int pick_gps(int ng) {
-  return ng % 4 == 0 ? 4 : ng % 5 == 0 ? 5 : ng % 3 == 0 ? 3 : ng % 2 == 0 ? 2 : 1;
-}
-
 // B fragment: 8 codes of one weight row as bf16 128+q, x_pairs order.
 __device__ __forceinline__ uint4 b_frag(uint32_t w) {
   uint32_t p[4];
@@ -141,264 +118,450 @@ __device__ __forceinline__ uint4 b_frag(uint32_t w) {
   return make_uint4(p[0], p[1], p[2], p[3]);
 }
 
-// One LDS pass of the A operand: 64 rows x (GPS groups of 64 inputs).
-// Thread work item j = (row, group): 128 contiguous bytes, consecutive
-// threads on consecutive groups of a row; rows past the tile read as zero.
-template <int GPS>
-struct AStage {
-  static constexpr int PAIRS = kTileM * GPS;
-  static constexpr int PER = (PAIRS + 255) / 256;
-  static constexpr int ROW = GPS * 8 + 1;   // uint4 per LDS row (+1 pad)
-  uint4 v[PER][8];
+// ---------------------------------------------------------------------------
+// The A operand's rows in x_pairs order (each 8-input piece p holds inputs
+// (0,4), (1,5), (2,6), (3,7) pairwise, the order of the B fragments) and their
+// 64-input row sums, once per call: one thread per piece, the 8 pieces of a
+// group in 8 consecutive lanes (rs: [rows][K / 64] fp32).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void grouped_prep_kernel(const uint16_t *__restrict__ src,
+                                                           int64_t rows, int K,
+                                                           uint16_t *__restrict__ dst,
+                                                           float *__restrict__ rs) {
+  // (32-bit index arithmetic: the host launches at most 2^30 pieces at a time)
+  const int ppr = K / 8;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const bool ok = i < (int)(rows * ppr);
+  const int r = ok ? i / ppr : 0;
+  const int pc = ok ? i - r * ppr : 0;
+  const uint4 v = ok ? load16(reinterpret_cast<const uint4 *>(src + (int64_t)r * K + pc * 8))
+                     : make_uint4(0, 0, 0, 0);
+  const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+  uint32_t out[4];
+  x_pairs(in, out);
+  float sm = 0.f;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) sm += bf16_to_f32(in[m] & 0xffffu) + bf16_to_f32(in[m] >> 16);
+  sm = group_sum<8>(sm);
+  if (ok) {
+    *reinterpret_cast<uint4 *>(dst + (int64_t)r * K + pc * 8) = make_uint4(out[0], out[1], out[2], out[3]);
+    if ((pc & 7) == 0) rs[(int64_t)r * (K / 64) + pc / 8] = sm;
+  }
+}
 
-  __device__ __forceinline__ void load(const uint16_t *const src[PER], int k0, int tid) {
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int pr = tid + 256 * j;
-      const bool ok = pr < PAIRS && src[j] != nullptr;
-      const uint4 *p =
-          ok ? reinterpret_cast<const uint4 *>(src[j] + k0 + (pr % GPS) * 64) : nullptr;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) v[j][q] = ok ? p[q] : make_uint4(0, 0, 0, 0);
-    }
+// ---------------------------------------------------------------------------
+// One work item of the grouped contraction: the rows of one tile (A, up to
+// 64 rows of KIN bf16 inputs, already in x_pairs order) against NPROJ
+// projections' 4-bit weights for NB consecutive output features.  WAVES
+// waves; wave w owns CPW 16-feature column blocks of every projection for
+// the NMB 16-row blocks the tile fills (a template parameter: no branches
+// around the MFMAs).
+//
+// Operands per 64-input quant group g:
+//  * A: the group's rows x 8 pieces, loaded RA - 1 groups ahead into a
+//    register ring and copied to LDS before the group's barrier: row-major,
+//    piece p of row r at r * 8 + (p ^ (r & 7)), so each 8-lane run of the
+//    copy writes one whole row (no bank conflict) and the MFMA reads of a
+//    piece across 16 rows fall on distinct banks.
+//  * B: the weights' codes of 4 groups at a time (a "quad", 128 bytes of
+//    every weight row: whole cache lines, 8 lanes per row), loaded BR quads
+//    ahead into registers and copied to LDS at the quad's first group.  Row
+//    layout in LDS: 8 chunks of 16 bytes, chunk c stored at c ^ (row & 7)
+//    with its two 8-byte halves swapped when row & 8, so the 16 rows read by
+//    one B-fragment load fall on distinct banks.  Each lane then reads its
+//    two code words (8 bytes) per group.
+// Every thread issues the same loads on every path (rows past the tile,
+// chunks past the row and refills past the end are either clamped to a
+// valid address and never used, or decided at compile time), so the
+// compiler's counter waits ask for exactly the data in hand while later
+// loads stay in flight.  The item's scales, biases and row sums are staged
+// in LDS once: scales quad-major (each lane reads its row's 4 scales of a
+// quad as 8 contiguous bytes, the 16 rows of a fragment side by side), row
+// sums at a pitch of 80 floats (the 4 groups of one bias MFMA on distinct
+// banks).  Each group accumulates into a fresh 16x16 block (2 MFMAs over
+// the bf16 128+q codes), folded into the output by S; the bias term
+// sum_g rowsum[g] * (B - 128 S) runs on fp32 MFMAs (K = 4 groups) at the end.
+// Rows past the tile compute garbage from a copy of a real row, which no
+// output row depends on (MFMA rows are independent) and nothing stores.
+// ---------------------------------------------------------------------------
+template <int KIN, int NB, int WAVES, int NPROJ, int RA_, int BR_>
+struct GItem {
+  static constexpr int NT = 64 * WAVES;
+  static constexpr int NG = KIN / 64;                  // quant groups along the inputs
+  static constexpr int NQ = (NG + 3) / 4;              // quads (B staging units)
+  static constexpr int NG4 = NQ;                       // bias MFMAs, 4 groups each
+  static constexpr int RA = RA_;                       // A ring slots (groups)
+  static constexpr int BR = BR_;                       // B register sets (quads)
+  static constexpr int CPW = NB / 16 / WAVES;          // column blocks per wave
+  static constexpr int SPT = (kTileM * 8 + NT - 1) / NT;   // A pieces per thread and group
+  static constexpr int BROWS = NPROJ * NB;             // weight rows of the item
+  static constexpr int BPT = BROWS * 8 / NT;           // B 16-byte pieces per thread and quad
+  static constexpr int SCB = NB * NG * 2;              // bytes of one scale array's block
+  static constexpr int NARR = 2 * NPROJ;               // (S, B) per projection
+  static constexpr int SCP = NARR * SCB / 16;          // 16-byte pieces of all of them
+  static constexpr int SCW = (SCP + NT - 1) / NT;      // ... per thread
+  // with NG a multiple of 4 the scales are staged quad-major: [array][quad][feature]
+  // x 4 halfwords (8-byte pieces), else copied as they are ([array][feature][group])
+  static constexpr bool QS = NG % 4 == 0;
+  static constexpr int SQP = NARR * NQ * NB;           // 8-byte pieces, quad-major
+  static constexpr int SQW = (SQP + NT - 1) / NT;      // ... per thread
+  static constexpr int RSW = (NG4 * 4 + WAVES - 1) / WAVES;   // row-sum groups per thread
+  static_assert(KIN % 64 == 0 && NB % (16 * WAVES) == 0 && CPW >= 1, "feature split");
+  static_assert(SCB % 16 == 0 && NT % 8 == 0 && (BROWS * 8) % NT == 0, "staging");
+  static_assert(8 % RA == 0 && RA >= 2 && (BR == 1 || BR == 2), "rings within an 8-group step");
+  // A refill at group g loads g + RA - 1; B refill at quad q loads q + BR.
+  // Steps of 8 groups [8t, 8t + 8) whose refills are all in range run as a
+  // loop (MAIN of them); the remaining groups are unrolled.
+  static constexpr bool step_full(int t) {
+    return 8 * t + 7 + RA - 1 < NG && 2 * t + 1 + BR < NQ;
   }
-  __device__ __forceinline__ void store(uint4 *a_l, float *rs_l, int tid) const {
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int pr = tid + 256 * j;
-      if (pr >= PAIRS) continue;
-      const int row = pr / GPS, grp = pr % GPS;
-      float s = 0.f;
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const uint32_t in[4] = {v[j][q].x, v[j][q].y, v[j][q].z, v[j][q].w};
-        uint32_t out[4];
-        x_pairs(in, out);
-        a_l[row * ROW + grp * 8 + q] = make_uint4(out[0], out[1], out[2], out[3]);
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-          s += bf16_to_f32(in[m] & 0xffffu) + bf16_to_f32(in[m] >> 16);
-      }
-      rs_l[grp * kTileM + row] = s;
-    }
+  static constexpr int main_steps() {
+    int t = 0;
+    while (step_full(t)) ++t;
+    return t;
   }
+  static constexpr int MAIN = main_steps();
 };
 
-// ---------------------------------------------------------------------------
-// grouped gate/up.  Work item = (tile, 64 features); 4 waves, wave w owns
-// features 16w..16w+15 of the block for every 16-row block of the tile.
-// Within a group, MFMA lane quarter kq takes code words 2kq and 2kq+1
-// (A pieces 2kq and 2kq+1 of the same group).
-// ---------------------------------------------------------------------------
-template <int D, int F, bool PBIAS>
-__global__ __launch_bounds__(256) void grouped_gate_up_kernel(
-    PoolArgs pa, const uint16_t *__restrict__ x, int k, const int32_t *__restrict__ perm,
-    const int4 *__restrict__ tiles, const int32_t *__restrict__ n_tiles,
-    uint16_t *__restrict__ h, int act, float alpha, float limit) {
-  constexpr int NG = D / 64, GPS = pick_gps(NG), NS = NG / GPS, NB = F / 64;
-  constexpr int NP = PBIAS ? 4 : 3;
-  using Stage = AStage<GPS>;
-  __shared__ uint4 a_l[kTileM * Stage::ROW];
-  __shared__ __align__(16) float rs_l[GPS * kTileM];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int col = lane & 15, kq = lane >> 4;
-  const int n_items = *n_tiles * NB;
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-    const int4 tl = tiles[item / NB];
-    const int ref = tl.x, r0 = tl.y, rows = tl.z;
-    const int n = (item % NB) * 64 + wave * 16 + col;   // this lane's feature
-    const char *gw = resolve(pa, comp_index(PROJ_GATE, PART_W, NP), ref);
-    if (gw == nullptr) {   // uniform over the workgroup
-      if (tid == 0) flag_error();
-      continue;
-    }
-    const uint2 *gwr = reinterpret_cast<const uint2 *>(gw) + (int64_t)n * (D / 16);
-    const uint2 *uwr =
-        reinterpret_cast<const uint2 *>(resolve(pa, comp_index(PROJ_UP, PART_W, NP), ref)) +
-        (int64_t)n * (D / 16);
-    const uint16_t *gs = reinterpret_cast<const uint16_t *>(
-                             resolve(pa, comp_index(PROJ_GATE, PART_S, NP), ref)) + (int64_t)n * NG;
-    const uint16_t *gb = reinterpret_cast<const uint16_t *>(
-                             resolve(pa, comp_index(PROJ_GATE, PART_B, NP), ref)) + (int64_t)n * NG;
-    const uint16_t *us = reinterpret_cast<const uint16_t *>(
-                             resolve(pa, comp_index(PROJ_UP, PART_S, NP), ref)) + (int64_t)n * NG;
-    const uint16_t *ub = reinterpret_cast<const uint16_t *>(
-                             resolve(pa, comp_index(PROJ_UP, PART_B, NP), ref)) + (int64_t)n * NG;
+struct GLds {   // (one layout for every instantiation; sized by the caller)
+  uint4 (*a)[kTileM * 8];  // [2][row * 8 + (piece ^ (row & 7))]
+  uint4 *b;                // [2][BROWS][8]: two quads of codes
+  float *rs;               // [NG4 * 4][kRsPitch]: 64-input row sums (row < 64), zero past NG
+  uint4 *sc;
+};
 
-    const uint16_t *src[Stage::PER];
+template <int NMB, int D, int F, bool PBIAS, int NB, int WAVES, int RA_, int BR_, bool GU>
+__device__ __forceinline__ void grouped_item(
+    const PoolArgs &pa, const uint16_t *__restrict__ aq, const float *__restrict__ ars, int k,
+    const int32_t *__restrict__ perm, int ref, int r0, int rows, int nb0,
+    uint16_t *__restrict__ h_out, const float *__restrict__ scores, float *__restrict__ yp,
+    int act, float alpha, float limit, const GLds &L) {
+  constexpr int KIN = GU ? D : F, NPROJ = GU ? 2 : 1;
+  using I = GItem<KIN, NB, WAVES, NPROJ, RA_, BR_>;
+  constexpr int NG = I::NG, NQ = I::NQ, CPW = I::CPW, NT = I::NT, SPT = I::SPT;
+  constexpr int RA = I::RA, BR = I::BR, BPT = I::BPT;
+  constexpr int NP = PBIAS ? 4 : 3, SCH = I::SCB / 2;   // halfwords per scale array block
+  constexpr int ROWS = NMB * 16;                        // staged rows
+  constexpr int RB = KIN / 2;                           // bytes per weight row
+  const uint16_t *sch = reinterpret_cast<const uint16_t *>(L.sc);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, kq = lane >> 4;
+  const char *w[NPROJ];
+  const char *sa[I::NARR];
 #pragma unroll
-    for (int j = 0; j < Stage::PER; ++j) {
-      const int row = (tid + 256 * j) / GPS;
-      src[j] = row < rows ? x + (int64_t)(perm[r0 + row] / k) * D : nullptr;
+  for (int j = 0; j < NPROJ; ++j) {
+    const int proj = GU ? (j == 0 ? PROJ_GATE : PROJ_UP) : PROJ_DOWN;
+    w[j] = resolve(pa, comp_index(proj, PART_W, NP), ref);
+    sa[2 * j] = resolve(pa, comp_index(proj, PART_S, NP), ref);
+    sa[2 * j + 1] = resolve(pa, comp_index(proj, PART_B, NP), ref);
+  }
+  // the A source row of tile row r (clamped into the tile)
+  auto src_row = [&](int r) -> int64_t {
+    r = min(r, rows - 1);
+    return GU ? perm[r0 + r] / k : r0 + r;
+  };
+  // this thread's A pieces (slot s = 8 * row + piece)
+  const uint16_t *asrc[SPT];
+#pragma unroll
+  for (int j = 0; j < SPT; ++j) {
+    const int s = tid + NT * j;
+    asrc[j] = aq + src_row(s >> 3) * KIN + (s & 7) * 8;
+  }
+  auto load_a = [&](int g, uint4 (&v)[SPT]) {
+#pragma unroll
+    for (int j = 0; j < SPT; ++j) v[j] = load16(reinterpret_cast<const uint4 *>(asrc[j] + g * 64));
+  };
+  // this thread's B pieces: piece p = tid + NT * i is chunk p % 8 of item
+  // weight row p / 8 (rows [0, NB) the first projection, then the second)
+  const char *bsrc[BPT];
+  uint32_t bdst[BPT];   // LDS byte offset of the piece's low half in a quad buffer
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) {
+    const int p = tid + NT * i, row = p >> 3, c = p & 7;
+    const int j = row / NB, fl = row % NB;
+    bsrc[i] = w[NPROJ > 1 ? j : 0] + (int64_t)(nb0 + fl) * RB + c * 16;
+    bdst[i] = (uint32_t)(row * 128 + ((c ^ (row & 7)) << 4) + ((row & 8) ? 8 : 0));
+  }
+  auto load_b = [&](int q, uint4 (&v)[BPT]) {
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) {
+      // (a chunk past the row end, in a last partial quad: any valid chunk)
+      const int off = (RB % 128 == 0 || q * 128 + 128 <= RB)
+                          ? q * 128
+                          : min(q * 128, RB - 16 - (int)((tid + NT * i) & 7) * 16);
+      v[i] = load16(reinterpret_cast<const uint4 *>(bsrc[i] + off));
     }
-    const int nmb = (rows + 15) / 16;
-    f32x4_t og[4], ou[4];
+  };
+  auto store_b = [&](int buf, const uint4 (&v)[BPT]) {
+    char *base = reinterpret_cast<char *>(L.b + buf * I::BROWS * 8);
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      og[mb] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-      ou[mb] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < BPT; ++i) {
+      // one 16-byte write per piece, halves swapped for rows with row & 8
+      const bool sw = (bdst[i] & 8) != 0;
+      const uint32_t x = v[i].x, y = v[i].y, z = v[i].z, w = v[i].w;
+      *reinterpret_cast<uint4 *>(base + (bdst[i] & ~8u)) =
+          make_uint4(sw ? z : x, sw ? w : y, sw ? x : z, sw ? y : w);
     }
-    Stage st;
-    st.load(src, 0, tid);
-    for (int s = 0; s < NS; ++s) {
-      uint2 wg[GPS], wu[GPS];
-      float Sg[GPS], Cg[GPS], Su[GPS], Cu[GPS];
+  };
+  // this lane's B fragment rows: feature col of column block cb, projection j
+  uint32_t bfr[NPROJ][CPW];   // LDS byte offset of the row in a quad buffer
+  uint32_t bx[NPROJ][CPW];    // its chunk swizzle (row & 7) and half swap (row & 8)
 #pragma unroll
-      for (int g = 0; g < GPS; ++g) {
-        const int gg = s * GPS + g;
-        wg[g] = gwr[gg * 4 + kq];
-        wu[g] = uwr[gg * 4 + kq];
-        Sg[g] = bf16_to_f32(gs[gg]);
-        Cg[g] = bf16_to_f32(gb[gg]) - 128.f * Sg[g];
-        Su[g] = bf16_to_f32(us[gg]);
-        Cu[g] = bf16_to_f32(ub[gg]) - 128.f * Su[g];
+  for (int j = 0; j < NPROJ; ++j)
+#pragma unroll
+    for (int cb = 0; cb < CPW; ++cb) {
+      const int row = j * NB + (wave * CPW + cb) * 16 + col;
+      bfr[j][cb] = row * 128;
+      bx[j][cb] = ((row & 7) << 4) | ((row & 8) ? 8 : 0);
+    }
+  // the item's scales and biases (each array's NB rows are one contiguous
+  // block) and row sums, loaded ahead of the rings and written to LDS after
+  constexpr bool QS = I::QS;
+  constexpr int SCN = QS ? I::SQW : I::SCW;
+  uint4 scv[QS ? 1 : I::SCW];
+  uint2 sqv[QS ? I::SQW : 1];
+#pragma unroll
+  for (int j = 0; j < SCN; ++j) {
+    if (QS) {   // piece i: feature i % NB, quad (i / NB) % NQ, array i / (NB * NQ)
+      const int i = min(tid + NT * j, I::SQP - 1);
+      const int nl = i % NB, q = (i / NB) % NQ, arr = i / (NB * NQ);
+      sqv[j] = *reinterpret_cast<const uint2 *>(sa[arr] + ((int64_t)(nb0 + nl) * NG + 4 * q) * 2);
+    } else {
+      const int i = min(tid + NT * j, I::SCP - 1);
+      const int arr = i / (I::SCB / 16), o = i % (I::SCB / 16);
+      scv[j] = load16(reinterpret_cast<const uint4 *>(sa[arr] + (int64_t)nb0 * NG * 2) + o);
+    }
+  }
+  float rsv[I::RSW];
+  {
+    const float *rrow = ars + src_row(lane) * NG;
+#pragma unroll
+    for (int j = 0; j < I::RSW; ++j) rsv[j] = rrow[min(wave + WAVES * j, NG - 1)];
+  }
+  uint4 breg[BR][BPT];
+#pragma unroll
+  for (int q = 0; q < BR; ++q)
+    if (q < NQ) load_b(q, breg[q]);
+  uint4 areg[RA][SPT];
+#pragma unroll
+  for (int i = 0; i + 1 < RA; ++i)
+    if (i < NG) load_a(i, areg[i]);
+#pragma unroll
+  for (int j = 0; j < SCN; ++j) {
+    if (QS) {
+      if (I::SQP % NT == 0 || tid + NT * j < I::SQP)
+        reinterpret_cast<uint2 *>(L.sc)[tid + NT * j] = sqv[j];
+    } else {
+      if (I::SCP % NT == 0 || tid + NT * j < I::SCP) L.sc[tid + NT * j] = scv[j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < I::RSW; ++j) {
+    const int g = wave + WAVES * j;
+    if (g < I::NG4 * 4) L.rs[g * kRsPitch + lane] = g < NG ? rsv[j] : 0.f;
+  }
+  f32x4_t acc[NMB][CPW][NPROJ];
+#pragma unroll
+  for (int rb = 0; rb < NMB; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < CPW; ++cb)
+#pragma unroll
+      for (int j = 0; j < NPROJ; ++j) acc[rb][cb][j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+  // with quad-major scales each lane reads its row's scales 4 groups at a
+  // time (8 bytes at the quad's first group)
+  const uint2 *scq = reinterpret_cast<const uint2 *>(L.sc);
+  uint2 s4[NPROJ][CPW];
+  // the bias term of quad q: fp32 MFMAs of K = 4 groups, A = row sums (lane:
+  // row col, group 4q + kq), B = B - 128 S of this lane's feature (zero past
+  // NG).  Each starts from a zero accumulator and is added on the VALU (no
+  // MFMA reads registers as its accumulator input: see below).
+  auto bias_step = [&](int q, const uint2 (&s4)[NPROJ][CPW]) {
+    const int gb = 4 * q + kq, gc = min(gb, NG - 1);
+    float C[NPROJ][CPW];
+#pragma unroll
+    for (int j = 0; j < NPROJ; ++j)
+#pragma unroll
+      for (int cb = 0; cb < CPW; ++cb) {
+        const int nl = (wave * CPW + cb) * 16 + col;
+        float sv, bv;
+        if (QS) {   // this lane's group of the quad from the quad's 4 halfwords
+          const uint2 b4 = scq[((2 * j + 1) * NQ + q) * NB + nl];
+          const uint32_t hs = kq < 2 ? s4[j][cb].x : s4[j][cb].y;
+          const uint32_t hb = kq < 2 ? b4.x : b4.y;
+          sv = __uint_as_float((kq & 1) ? (hs & 0xffff0000u) : (hs << 16));
+          bv = __uint_as_float((kq & 1) ? (hb & 0xffff0000u) : (hb << 16));
+        } else {
+          sv = bf16_to_f32(sch[(2 * j) * SCH + nl * NG + gc]);
+          bv = bf16_to_f32(sch[(2 * j + 1) * SCH + nl * NG + gc]);
+        }
+        C[j][cb] = gb < NG ? bv - 128.f * sv : 0.f;
       }
-      __syncthreads();   // the previous pass's LDS reads are done
-      st.store(a_l, rs_l, tid);
-      __syncthreads();
-      if (s + 1 < NS) st.load(src, (s + 1) * GPS * 64, tid);
 #pragma unroll
-      for (int g = 0; g < GPS; ++g) {
-        const uint4 bg0 = b_frag(wg[g].x), bg1 = b_frag(wg[g].y);
-        const uint4 bu0 = b_frag(wu[g].x), bu1 = b_frag(wu[g].y);
+    for (int rb = 0; rb < NMB; ++rb) {
+      const float ra = L.rs[gb * kRsPitch + rb * 16 + col];
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          if (mb >= nmb) break;
-          const uint4 *ar = a_l + (mb * 16 + col) * Stage::ROW + g * 8 + 2 * kq;
-          const uint4 a0 = ar[0], a1 = ar[1];
-          f32x4_t cg = {0.f, 0.f, 0.f, 0.f}, cu = {0.f, 0.f, 0.f, 0.f};
-          cg = mfma16x16x32(a0, bg0, cg);
-          cg = mfma16x16x32(a1, bg1, cg);
-          cu = mfma16x16x32(a0, bu0, cu);
-          cu = mfma16x16x32(a1, bu1, cu);
+      for (int cb = 0; cb < CPW; ++cb)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            og[mb][r] += Sg[g] * cg[r];
-            ou[mb][r] += Su[g] * cu[r];
-          }
+        for (int j = 0; j < NPROJ; ++j) {
+          const f32x4_t bz = __builtin_amdgcn_mfma_f32_16x16x4f32(
+              ra, C[j][cb], (f32x4_t){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[rb][cb][j][e] += bz[e];
+        }
+    }
+  };
+  // one group (gi: g mod 8, known at compile time in every unrolled copy;
+  // the refill and bias flags likewise)
+  auto group = [&](int g, int gi, bool a_refill, bool b_refill, bool bias_now) {
+    if (gi % 4 == 0) {   // a quad starts: its codes to LDS, refill their registers
+      const int q = g >> 2, bs = (gi / 4) % BR;
+      store_b(q & 1, breg[bs]);
+      if (b_refill) load_b(q + BR, breg[bs]);
+    }
+    uint4 *al = L.a[g & 1];
+    const int s = gi % RA;
+#pragma unroll
+    for (int j = 0; j < SPT; ++j) {
+      const int sl = tid + NT * j;
+      if (sl < ROWS * 8) {   // uniform per wave
+        const int r = sl >> 3, p = sl & 7;
+        al[r * 8 + (p ^ (r & 7))] = areg[s][j];
+      }
+    }
+    __syncthreads();
+    if (a_refill) load_a(g + RA - 1, areg[(s + RA - 1) % RA]);
+    if (QS && gi % 4 == 0) {   // the quad's scales, 4 halfwords per lane and row
+#pragma unroll
+      for (int j = 0; j < NPROJ; ++j)
+#pragma unroll
+        for (int cb = 0; cb < CPW; ++cb) {
+          const int nl = (wave * CPW + cb) * 16 + col;
+          s4[j][cb] = scq[((2 * j) * NQ + (g >> 2)) * NB + nl];
+        }
+    }
+    const char *bq = reinterpret_cast<const char *>(L.b + ((g >> 2) & 1) * I::BROWS * 8);
+    const uint32_t cpos = (uint32_t)((gi % 4) * 32 + kq * 8);   // logical chunk and half
+    uint4 b0[NPROJ][CPW], b1[NPROJ][CPW];
+    float S[NPROJ][CPW];
+#pragma unroll
+    for (int j = 0; j < NPROJ; ++j)
+#pragma unroll
+      for (int cb = 0; cb < CPW; ++cb) {
+        const uint2 cw = *reinterpret_cast<const uint2 *>(bq + bfr[j][cb] + (cpos ^ bx[j][cb]));
+        b0[j][cb] = b_frag(cw.x);
+        b1[j][cb] = b_frag(cw.y);
+        if (QS) {
+          const uint32_t h = (gi % 4) < 2 ? s4[j][cb].x : s4[j][cb].y;
+          S[j][cb] = __uint_as_float((gi & 1) ? (h & 0xffff0000u) : (h << 16));
+        } else {
+          const int nl = (wave * CPW + cb) * 16 + col;
+          S[j][cb] = bf16_to_f32(sch[(2 * j) * SCH + nl * NG + g]);
         }
       }
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        if (mb >= nmb) break;
-        bias_term<GPS>(rs_l, Cg, mb, col, kq, og[mb]);
-        bias_term<GPS>(rs_l, Cu, mb, col, kq, ou[mb]);
+    for (int rb = 0; rb < NMB; ++rb) {
+      const int r = rb * 16 + col;
+      const uint4 a0 = al[r * 8 + ((2 * kq) ^ (r & 7))], a1 = al[r * 8 + ((2 * kq + 1) ^ (r & 7))];
+#pragma unroll
+      for (int cb = 0; cb < CPW; ++cb)
+#pragma unroll
+        for (int j = 0; j < NPROJ; ++j) {
+          const f32x4_t c0 = mfma16x16x32(a0, b0[j][cb], (f32x4_t){0.f, 0.f, 0.f, 0.f});
+          const f32x4_t c = mfma16x16x32(a1, b1[j][cb], c0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[rb][cb][j][e] += S[j][cb] * c[e];
+          // c0 (the second MFMA's accumulator input) stays allocated until the
+          // fold has read c: this compiler otherwise reuses its registers a
+          // few instructions after the MFMA issues, before the MFMA has read
+          // them
+          asm volatile("" ::"v"(c0), "v"(acc[rb][cb][j]));
+        }
+    }
+    if (bias_now) bias_step(g >> 2, s4);   // the quad's last group
+  };
+  for (int g0 = 0; g0 < I::MAIN * 8; g0 += 8) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) group(g0 + i, i, true, true, i % 4 == 3);
+  }
+#pragma unroll
+  for (int g = I::MAIN * 8; g < NG; ++g)
+    group(g, g % 8, g + RA - 1 < NG, (g >> 2) + BR < NQ, g % 4 == 3 || g == NG - 1);
+  // epilogue
+#pragma unroll
+  for (int cb = 0; cb < CPW; ++cb) {
+    const int n = nb0 + (wave * CPW + cb) * 16 + col;
+    float pb[NPROJ];
+#pragma unroll
+    for (int j = 0; j < NPROJ; ++j) {
+      pb[j] = 0.f;
+      if (PBIAS) {
+        const int proj = GU ? (j == 0 ? PROJ_GATE : PROJ_UP) : PROJ_DOWN;
+        pb[j] = bf16_to_f32(reinterpret_cast<const uint16_t *>(
+            resolve(pa, comp_index(proj, PART_BIAS, NP), ref))[n]);
       }
     }
-    float pbg = 0.f, pbu = 0.f;
-    if (PBIAS) {
-      pbg = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-          resolve(pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref))[n]);
-      pbu = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-          resolve(pa, comp_index(PROJ_UP, PART_BIAS, NP), ref))[n]);
-    }
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int rb = 0; rb < NMB; ++rb) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int rr = mb * 16 + 4 * kq + r;
+      for (int e = 0; e < 4; ++e) {
+        const int rr = rb * 16 + 4 * kq + e;
         if (rr < rows) {
-          const float hv = apply_act(act, og[mb][r] + pbg, ou[mb][r] + pbu, alpha, limit);
-          h[(int64_t)(r0 + rr) * F + n] = (uint16_t)f32_to_bf16(hv);
+          if (GU) {
+            const float hv = apply_act(act, acc[rb][cb][0][e] + pb[0],
+                                       acc[rb][cb][NPROJ - 1][e] + pb[NPROJ - 1], alpha, limit);
+            h_out[(int64_t)(r0 + rr) * F + n] = (uint16_t)f32_to_bf16(hv);
+          } else {
+            const int pr = perm[r0 + rr];
+            yp[(int64_t)pr * D + n] = scores[pr] * (acc[rb][cb][0][e] + pb[0]);
+          }
         }
       }
     }
   }
 }
 
-// ---------------------------------------------------------------------------
-// grouped down.  Work item = (tile, 64 outputs of d_model); A = the tile's h
-// rows (sorted order); Yp[pair, n] = score[pair] * (h . Wd[n] + bias[n]).
-// ---------------------------------------------------------------------------
-template <int D, int F, bool PBIAS>
-__global__ __launch_bounds__(256) void grouped_down_kernel(
-    PoolArgs pa, const uint16_t *__restrict__ h, const float *__restrict__ scores,
+template <int D, int F, bool PBIAS, int NB, int WAVES, int RA, int BR, bool GU>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2))) void grouped_mm_kernel(
+    PoolArgs pa, const uint16_t *__restrict__ aq, const float *__restrict__ ars, int k,
     const int32_t *__restrict__ perm, const int4 *__restrict__ tiles,
-    const int32_t *__restrict__ n_tiles, float *__restrict__ yp) {
-  constexpr int NG = F / 64, GPS = pick_gps(NG), NS = NG / GPS, NB = D / 64;
-  constexpr int NP = PBIAS ? 4 : 3;
-  using Stage = AStage<GPS>;
-  __shared__ uint4 a_l[kTileM * Stage::ROW];
-  __shared__ __align__(16) float rs_l[GPS * kTileM];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int col = lane & 15, kq = lane >> 4;
-  const int n_items = *n_tiles * NB;
+    const int32_t *__restrict__ n_tiles, uint16_t *__restrict__ h_out,
+    const float *__restrict__ scores, float *__restrict__ yp, int act, float alpha,
+    float limit) {
+  constexpr int KIN = GU ? D : F, NOUT = GU ? F : D, NPROJ = GU ? 2 : 1;
+  constexpr int NBK = NOUT / NB, NP = PBIAS ? 4 : 3;
+  using I = GItem<KIN, NB, WAVES, NPROJ, RA, BR>;
+  static_assert(NOUT % NB == 0, "whole feature blocks");
+  __shared__ uint4 a_l[2][kTileM * 8];
+  __shared__ uint4 b_l[2 * I::BROWS * 8];
+  __shared__ float rs_l[I::NG4 * 4 * kRsPitch];
+  __shared__ uint4 sc_l[I::QS ? (I::SQP + 1) / 2 : I::SCP];
+  const GLds L{a_l, b_l, rs_l, sc_l};
+  const int n_items = *n_tiles * NBK;
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-    const int4 tl = tiles[item / NB];
+    const int4 tl = tiles[item / NBK];
     const int ref = tl.x, r0 = tl.y, rows = tl.z;
-    const int n = (item % NB) * 64 + wave * 16 + col;
-    const char *dw = resolve(pa, comp_index(PROJ_DOWN, PART_W, NP), ref);
-    if (dw == nullptr) {
-      if (tid == 0) flag_error();
+    const int nb0 = (item % NBK) * NB;
+    bool bad = false;
+#pragma unroll
+    for (int j = 0; j < NPROJ; ++j) {
+      const int proj = GU ? (j == 0 ? PROJ_GATE : PROJ_UP) : PROJ_DOWN;
+      bad = bad || resolve(pa, comp_index(proj, PART_W, NP), ref) == nullptr;
+    }
+    if (bad) {   // uniform over the workgroup
+      if (threadIdx.x == 0) flag_error();
       continue;
     }
-    const uint2 *dwr = reinterpret_cast<const uint2 *>(dw) + (int64_t)n * (F / 16);
-    const uint16_t *ds = reinterpret_cast<const uint16_t *>(
-                             resolve(pa, comp_index(PROJ_DOWN, PART_S, NP), ref)) + (int64_t)n * NG;
-    const uint16_t *db = reinterpret_cast<const uint16_t *>(
-                             resolve(pa, comp_index(PROJ_DOWN, PART_B, NP), ref)) + (int64_t)n * NG;
-
-    const uint16_t *src[Stage::PER];
-#pragma unroll
-    for (int j = 0; j < Stage::PER; ++j) {
-      const int row = (tid + 256 * j) / GPS;
-      src[j] = row < rows ? h + (int64_t)(r0 + row) * F : nullptr;
-    }
-    const int nmb = (rows + 15) / 16;
-    f32x4_t o[4];
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) o[mb] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    Stage st;
-    st.load(src, 0, tid);
-    for (int s = 0; s < NS; ++s) {
-      uint2 w[GPS];
-      float S[GPS], C[GPS];
-#pragma unroll
-      for (int g = 0; g < GPS; ++g) {
-        const int gg = s * GPS + g;
-        w[g] = dwr[gg * 4 + kq];
-        S[g] = bf16_to_f32(ds[gg]);
-        C[g] = bf16_to_f32(db[gg]) - 128.f * S[g];
-      }
-      __syncthreads();
-      st.store(a_l, rs_l, tid);
-      __syncthreads();
-      if (s + 1 < NS) st.load(src, (s + 1) * GPS * 64, tid);
-#pragma unroll
-      for (int g = 0; g < GPS; ++g) {
-        const uint4 b0 = b_frag(w[g].x), b1 = b_frag(w[g].y);
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          if (mb >= nmb) break;
-          const uint4 *ar = a_l + (mb * 16 + col) * Stage::ROW + g * 8 + 2 * kq;
-          f32x4_t c = {0.f, 0.f, 0.f, 0.f};
-          c = mfma16x16x32(ar[0], b0, c);
-          c = mfma16x16x32(ar[1], b1, c);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) o[mb][r] += S[g] * c[r];
-        }
-      }
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        if (mb >= nmb) break;
-        bias_term<GPS>(rs_l, C, mb, col, kq, o[mb]);
-      }
-    }
-    float pb = 0.f;
-    if (PBIAS)
-      pb = bf16_to_f32(reinterpret_cast<const uint16_t *>(
-          resolve(pa, comp_index(PROJ_DOWN, PART_BIAS, NP), ref))[n]);
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int rr = mb * 16 + 4 * kq + r;
-        if (rr < rows) {
-          const int p = perm[r0 + rr];
-          yp[(int64_t)p * D + n] = scores[p] * (o[mb][r] + pb);
-        }
-      }
-    }
+    const int nmb = (rows + 15) >> 4;
+#define MOE_GITEM(M)                                                                      \
+  grouped_item<M, D, F, PBIAS, NB, WAVES, RA, BR, GU>(pa, aq, ars, k, perm, ref, r0, rows, nb0, h_out, \
+                                              scores, yp, act, alpha, limit, L)
+    if (nmb == 1) MOE_GITEM(1);
+    else if (nmb == 2) MOE_GITEM(2);
+    else if (nmb == 3) MOE_GITEM(3);
+    else MOE_GITEM(4);
+#undef MOE_GITEM
+    __syncthreads();   // the LDS of this item is read before the next item stages
   }
 }
 
@@ -426,29 +589,33 @@ __global__ __launch_bounds__(256) void combine_pairs_kernel(
 }
 
 // ---------------------------------------------------------------------------
-template <int D, int F, bool PB>
-static void launch_gg(dim3 g, hipStream_t s, const PoolArgs &pa, const uint16_t *x, int k,
-                      const int32_t *perm, const int4 *tiles, const int32_t *nt, uint16_t *h,
-                      int act, float alpha, float limit) {
-  hipLaunchKernelGGL((grouped_gate_up_kernel<D, F, PB>), g, dim3(256), 0, s, pa, x, k, perm,
-                     tiles, nt, h, act, alpha, limit);
+template <int D, int F, bool PB, int NBU, int WU, int RU, int BU>
+static void launch_gg(dim3 g, hipStream_t s, const PoolArgs &pa, const uint16_t *xq,
+                      const float *rsx, int k, const int32_t *perm, const int4 *tiles,
+                      const int32_t *nt, uint16_t *h, int act, float alpha, float limit) {
+  hipLaunchKernelGGL((grouped_mm_kernel<D, F, PB, NBU, WU, RU, BU, true>), g, dim3(64 * WU), 0, s, pa,
+                     xq, rsx, k, perm, tiles, nt, h, nullptr, nullptr, act, alpha, limit);
 }
-template <int D, int F, bool PB>
-static void launch_gd(dim3 g, hipStream_t s, const PoolArgs &pa, const uint16_t *h,
-                      const float *sc, const int32_t *perm, const int4 *tiles,
-                      const int32_t *nt, float *yp) {
-  hipLaunchKernelGGL((grouped_down_kernel<D, F, PB>), g, dim3(256), 0, s, pa, h, sc, perm,
-                     tiles, nt, yp);
+template <int D, int F, bool PB, int NBD, int WD, int RD, int BD>
+static void launch_gd(dim3 g, hipStream_t s, const PoolArgs &pa, const uint16_t *hq,
+                      const float *rsh, const float *sc, const int32_t *perm,
+                      const int4 *tiles, const int32_t *nt, float *yp) {
+  hipLaunchKernelGGL((grouped_mm_kernel<D, F, PB, NBD, WD, RD, BD, false>), g, dim3(64 * WD), 0, s,
+                     pa, hq, rsh, 1, perm, tiles, nt, nullptr, sc, yp, 0, 0.f, 0.f);
 }
 
-#define MOE_GROUPED_GEOM(D, F, PB) {D, F, PB, &launch_gg<D, F, PB>, &launch_gd<D, F, PB>}
+// (features per work item, waves, A ring depth in groups, B register sets in
+// quads) of gate/up and of down per geometry
+#define MOE_GROUPED_GEOM(D, F, PB, NBU, WU, RU, BU, NBD, WD, RD, BD)                    \
+  {D, F, PB, NBU, NBD, &launch_gg<D, F, PB, NBU, WU, RU, BU>,                             \
+   &launch_gd<D, F, PB, NBD, WD, RD, BD>}
 static const GroupedLaunch kGroupedTable[] = {
-    MOE_GROUPED_GEOM(2048, 768, false),   // Qwen3-30B-A3B
-    MOE_GROUPED_GEOM(2048, 768, true),
-    MOE_GROUPED_GEOM(2880, 2880, true),   // gpt-oss-120b
-    MOE_GROUPED_GEOM(2880, 2880, false),
-    MOE_GROUPED_GEOM(256, 128, false),    // small test geometry
-    MOE_GROUPED_GEOM(256, 128, true),
+    MOE_GROUPED_GEOM(2048, 768, false, 64, 4, 8, 1, 64, 4, 4, 1),   // Qwen3-30B-A3B
+    MOE_GROUPED_GEOM(2048, 768, true, 64, 4, 8, 1, 64, 4, 4, 1),
+    MOE_GROUPED_GEOM(2880, 2880, true, 96, 6, 4, 2, 192, 6, 4, 2),   // gpt-oss-120b
+    MOE_GROUPED_GEOM(2880, 2880, false, 96, 6, 4, 2, 192, 6, 4, 2),
+    MOE_GROUPED_GEOM(256, 128, false, 128, 8, 4, 1, 128, 8, 2, 1),   // small test geometry
+    MOE_GROUPED_GEOM(256, 128, true, 128, 8, 4, 1, 128, 8, 2, 1),
 };
 
 const GroupedLaunch *find_grouped(int d_model, int d_ff, int has_bias) {
@@ -468,8 +635,24 @@ GroupedWs grouped_ws(int64_t T, int k, int D, int F) {
   w.off_ntiles = o; o += al(4);
   w.off_h = o; o += al((size_t)P * F * 2);
   w.off_yp = o; o += al((size_t)P * D * 4);
+  w.off_xq = o; o += al((size_t)T * D * 2);
+  w.off_rsx = o; o += al((size_t)T * (D / 64) * 4);
+  w.off_hq = o; o += al((size_t)P * F * 2);
+  w.off_rsh = o; o += al((size_t)P * (F / 64) * 4);
   w.total = o;
   return w;
+}
+
+// (in launches of at most 2^30 pieces, so the kernel's indices fit 32 bits)
+static void launch_prep(const uint16_t *src, int64_t rows, int K, uint16_t *dst, float *rs,
+                        hipStream_t s) {
+  const int64_t chunk = ((int64_t)1 << 30) / (K / 8);
+  for (int64_t r0 = 0; r0 < rows; r0 += chunk) {
+    const int64_t nr = std::min(chunk, rows - r0);
+    const int64_t n = nr * (K / 8);
+    hipLaunchKernelGGL(grouped_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                       src + r0 * K, nr, K, dst + r0 * K, rs + r0 * (K / 64));
+  }
 }
 
 void launch_grouped(const GroupedLaunch *G, const PoolArgs &pa, const int32_t *refs,
@@ -483,13 +666,19 @@ void launch_grouped(const GroupedLaunch *G, const PoolArgs &pa, const int32_t *r
   int32_t *ntiles = reinterpret_cast<int32_t *>(ws + w.off_ntiles);
   uint16_t *h = reinterpret_cast<uint16_t *>(ws + w.off_h);
   float *yp = reinterpret_cast<float *>(ws + w.off_yp);
+  uint16_t *xq = reinterpret_cast<uint16_t *>(ws + w.off_xq);
+  float *rsx = reinterpret_cast<float *>(ws + w.off_rsx);
+  uint16_t *hq = reinterpret_cast<uint16_t *>(ws + w.off_hq);
+  float *rsh = reinterpret_cast<float *>(ws + w.off_rsh);
   const int nkeys = pa.n_slots + pa.n_records;
   hipLaunchKernelGGL(group_pairs_kernel, dim3(1), dim3(1024), (size_t)nkeys * 4, s, refs, P,
                      pa.n_slots, pa.n_records, D, perm, tiles, ntiles, yp);
-  const int64_t items_up = w.max_tiles * (F / 64), items_down = w.max_tiles * (D / 64);
-  G->gate_up(dim3((unsigned)std::min<int64_t>(items_up, kGroupedMaxWGs)), s, pa, x, k, perm,
+  launch_prep(x, T, D, xq, rsx, s);
+  const int64_t items_up = w.max_tiles * (F / G->nb_up), items_down = w.max_tiles * (D / G->nb_down);
+  G->gate_up(dim3((unsigned)std::min<int64_t>(items_up, kGroupedMaxWGs)), s, pa, xq, rsx, k, perm,
              tiles, ntiles, h, act, alpha, limit);
-  G->down(dim3((unsigned)std::min<int64_t>(items_down, kGroupedMaxWGs)), s, pa, h, scores,
+  launch_prep(h, P, F, hq, rsh, s);
+  G->down(dim3((unsigned)std::min<int64_t>(items_down, kGroupedMaxWGs)), s, pa, hq, rsh, scores,
           perm, tiles, ntiles, yp);
   const int64_t n4 = (int64_t)T * D / 4;
   hipLaunchKernelGGL(combine_pairs_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,

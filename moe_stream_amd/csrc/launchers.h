@@ -69,15 +69,16 @@ constexpr int kGroupMaxKeys = 16256;    // n_slots + n_records: LDS histogram <=
 constexpr int kGroupedMaxWGs = 2048;    // grid cap; workgroups loop over items
 struct GroupedLaunch {
   int d_model, d_ff, has_bias;
-  void (*gate_up)(dim3, hipStream_t, const PoolArgs &, const uint16_t *, int,
+  int nb_up, nb_down;   // output features per work item of gate/up and of down
+  void (*gate_up)(dim3, hipStream_t, const PoolArgs &, const uint16_t *, const float *, int,
                   const int32_t *, const int4 *, const int32_t *, uint16_t *, int, float,
                   float);
   void (*down)(dim3, hipStream_t, const PoolArgs &, const uint16_t *, const float *,
-               const int32_t *, const int4 *, const int32_t *, float *);
+               const float *, const int32_t *, const int4 *, const int32_t *, float *);
 };
 struct GroupedWs {
   int64_t max_tiles;
-  size_t off_perm, off_tiles, off_ntiles, off_h, off_yp, total;
+  size_t off_perm, off_tiles, off_ntiles, off_h, off_yp, off_xq, off_rsx, off_hq, off_rsh, total;
 };
 const GroupedLaunch *find_grouped(int d_model, int d_ff, int has_bias);
 GroupedWs grouped_ws(int64_t T, int k, int D, int F);
