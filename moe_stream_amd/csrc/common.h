@@ -24,6 +24,26 @@ __device__ __forceinline__ uint4 load16(const uint4 *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Loads through a pointer the compiler cannot place (one built from pool or
+// store bases): as global loads.  A generic (flat) load also counts on the
+// LDS counter, so every LDS wait (each workgroup barrier among them) would
+// wait for it too.
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 gload16(const void *p) {
+  const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t *)(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 gload8(const void *p) {
+  const u32x2_t v = *(const __attribute__((address_space(1))) u32x2_t *)(p);
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ float gload4f(const void *p) {
+  return *(const __attribute__((address_space(1))) float *)(p);
+}
+__device__ __forceinline__ int gload4i(const void *p) {
+  return *(const __attribute__((address_space(1))) int *)(p);
+}
+
 __device__ __forceinline__ uint4 load_stream16(const uint4 *p) {
   u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
   return make_uint4(v.x, v.y, v.z, v.w);

@@ -61,7 +61,9 @@ __global__ __launch_bounds__(1024) void group_pairs_kernel(
     int32_t *__restrict__ perm, int4 *__restrict__ tiles, int32_t *__restrict__ n_tiles,
     float *__restrict__ yp) {
   extern __shared__ int hist[];
-  __shared__ int wsum_p[16], wsum_t[16];
+  // tiles are listed by size class, largest first (classes 4..1: a tile of
+  // r rows is class ceil(r / 16)), so the longest work items start first
+  __shared__ int wsum_p[16], wsum_t[4][16], cbase[5];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nkeys = n_slots + n_records;
   for (int i = tid; i < nkeys; i += 1024) hist[i] = 0;
@@ -76,32 +78,57 @@ __global__ __launch_bounds__(1024) void group_pairs_kernel(
     }
   }
   __syncthreads();
-  // per-thread contiguous key chunk: pair and tile totals, then a block scan
+  // per-thread contiguous key chunk: pair and per-class tile totals, then
+  // block scans
   const int chunk = (nkeys + 1023) / 1024;
   const int k0 = min(tid * chunk, nkeys), k1 = min(k0 + chunk, nkeys);
-  int sp = 0, st = 0;
+  auto tile_class = [](int rows) { return (rows + 15) >> 4; };   // 1..4
+  int sp = 0, st[4] = {0, 0, 0, 0};
   for (int i = k0; i < k1; ++i) {
     const int c = hist[i];
     sp += c;
-    st += (c + kTileM - 1) / kTileM;
+    st[3] += c / kTileM;
+    if (c % kTileM) ++st[tile_class(c % kTileM) - 1];
   }
-  const int ip = wave_incl_scan(sp, lane), it = wave_incl_scan(st, lane);
+  const int ip = wave_incl_scan(sp, lane);
+  int it[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) it[q] = wave_incl_scan(st[q], lane);
   if (lane == 63) {
     wsum_p[wave] = ip;
-    wsum_t[wave] = it;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) wsum_t[q][wave] = it[q];
   }
   __syncthreads();
-  int bp = ip - sp, bt = it - st;
+  if (tid == 0) {   // class bases: class 4 first
+    int b = 0;
+    for (int q = 3; q >= 0; --q) {
+      cbase[q] = b;
+      for (int w = 0; w < 16; ++w) b += wsum_t[q][w];
+    }
+    cbase[4] = b;
+    *n_tiles = b;
+  }
+  __syncthreads();
+  int bp = ip - sp, bt[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) bt[q] = cbase[q] + it[q] - st[q];
   for (int w = 0; w < wave; ++w) {
     bp += wsum_p[w];
-    bt += wsum_t[w];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) bt[q] += wsum_t[q][w];
   }
-  if (tid == 1023) *n_tiles = bt + st;
   for (int i = k0; i < k1; ++i) {
     const int c = hist[i];
     hist[i] = bp;   // becomes the scatter cursor of key i
-    for (int m = 0; m < c; m += kTileM)
-      tiles[bt++] = make_int4(i - n_records, bp + m, min(kTileM, c - m), 0);
+    for (int m = 0; m < c; m += kTileM) {
+      const int rows = min(kTileM, c - m), q = tile_class(rows) - 1;
+      int t = 0;
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq)   // (registers, not a dynamic index)
+        if (qq == q) t = bt[qq]++;
+      tiles[t] = make_int4(i - n_records, bp + m, rows, 0);
+    }
     bp += c;
   }
   __syncthreads();
@@ -224,6 +251,7 @@ struct GItem {
 };
 
 struct GLds {   // (one layout for every instantiation; sized by the caller)
+  float *part;             // gate/up with the fused input prep: [NB / 16][64] row partial sums
   uint4 (*a)[kTileM * 8];  // [2][row * 8 + (piece ^ (row & 7))]
   uint4 *b;                // [2][BROWS][8]: two quads of codes
   float *rs;               // [NG4 * 4][kRsPitch]: 64-input row sums (row < 64), zero past NG
@@ -234,8 +262,8 @@ template <int NMB, int D, int F, bool PBIAS, int NB, int WAVES, int RA_, int BR_
 __device__ __forceinline__ void grouped_item(
     const PoolArgs &pa, const uint16_t *__restrict__ aq, const float *__restrict__ ars, int k,
     const int32_t *__restrict__ perm, int ref, int r0, int rows, int nb0,
-    uint16_t *__restrict__ h_out, const float *__restrict__ scores, float *__restrict__ yp,
-    int act, float alpha, float limit, const GLds &L) {
+    uint16_t *__restrict__ h_out, float *__restrict__ rs_out, const float *__restrict__ scores,
+    float *__restrict__ yp, int act, float alpha, float limit, const GLds &L) {
   constexpr int KIN = GU ? D : F, NPROJ = GU ? 2 : 1;
   using I = GItem<KIN, NB, WAVES, NPROJ, RA_, BR_>;
   constexpr int NG = I::NG, NQ = I::NQ, CPW = I::CPW, NT = I::NT, SPT = I::SPT;
@@ -259,7 +287,7 @@ __device__ __forceinline__ void grouped_item(
   // the A source row of tile row r (clamped into the tile)
   auto src_row = [&](int r) -> int64_t {
     r = min(r, rows - 1);
-    return GU ? perm[r0 + r] / k : r0 + r;
+    return GU ? gload4i(perm + r0 + r) / k : r0 + r;
   };
   // this thread's A pieces (slot s = 8 * row + piece)
   const uint16_t *asrc[SPT];
@@ -270,7 +298,7 @@ __device__ __forceinline__ void grouped_item(
   }
   auto load_a = [&](int g, uint4 (&v)[SPT]) {
 #pragma unroll
-    for (int j = 0; j < SPT; ++j) v[j] = load16(reinterpret_cast<const uint4 *>(asrc[j] + g * 64));
+    for (int j = 0; j < SPT; ++j) v[j] = gload16(asrc[j] + g * 64);
   };
   // this thread's B pieces: piece p = tid + NT * i is chunk p % 8 of item
   // weight row p / 8 (rows [0, NB) the first projection, then the second)
@@ -290,7 +318,7 @@ __device__ __forceinline__ void grouped_item(
       const int off = (RB % 128 == 0 || q * 128 + 128 <= RB)
                           ? q * 128
                           : min(q * 128, RB - 16 - (int)((tid + NT * i) & 7) * 16);
-      v[i] = load16(reinterpret_cast<const uint4 *>(bsrc[i] + off));
+      v[i] = gload16(bsrc[i] + off);
     }
   };
   auto store_b = [&](int buf, const uint4 (&v)[BPT]) {
@@ -326,18 +354,18 @@ __device__ __forceinline__ void grouped_item(
     if (QS) {   // piece i: feature i % NB, quad (i / NB) % NQ, array i / (NB * NQ)
       const int i = min(tid + NT * j, I::SQP - 1);
       const int nl = i % NB, q = (i / NB) % NQ, arr = i / (NB * NQ);
-      sqv[j] = *reinterpret_cast<const uint2 *>(sa[arr] + ((int64_t)(nb0 + nl) * NG + 4 * q) * 2);
+      sqv[j] = gload8(sa[arr] + ((int64_t)(nb0 + nl) * NG + 4 * q) * 2);
     } else {
       const int i = min(tid + NT * j, I::SCP - 1);
       const int arr = i / (I::SCB / 16), o = i % (I::SCB / 16);
-      scv[j] = load16(reinterpret_cast<const uint4 *>(sa[arr] + (int64_t)nb0 * NG * 2) + o);
+      scv[j] = gload16(sa[arr] + (int64_t)nb0 * NG * 2 + (int64_t)o * 16);
     }
   }
   float rsv[I::RSW];
   {
     const float *rrow = ars + src_row(lane) * NG;
 #pragma unroll
-    for (int j = 0; j < I::RSW; ++j) rsv[j] = rrow[min(wave + WAVES * j, NG - 1)];
+    for (int j = 0; j < I::RSW; ++j) rsv[j] = gload4f(rrow + min(wave + WAVES * j, NG - 1));
   }
   uint4 breg[BR][BPT];
 #pragma unroll
@@ -487,10 +515,16 @@ __device__ __forceinline__ void grouped_item(
 #pragma unroll
   for (int g = I::MAIN * 8; g < NG; ++g)
     group(g, g % 8, g + RA - 1 < NG, (g >> 2) + BR < NQ, g % 4 == 3 || g == NG - 1);
-  // epilogue
+  // epilogue.  Gate/up with NB a multiple of 64 also does the down kernel's
+  // input prep: h goes out in x_pairs order (feature f of an 8-feature piece
+  // at 2 * (f % 4) + f / 4) with the sums of its bf16 values over each
+  // 64-feature group (16 features per 16-lane row, then 4 column blocks in
+  // order through LDS).
+  constexpr bool FUSE = GU && NB % 64 == 0;
 #pragma unroll
   for (int cb = 0; cb < CPW; ++cb) {
     const int n = nb0 + (wave * CPW + cb) * 16 + col;
+    const int np = FUSE ? (n & ~7) + ((n & 3) << 1) + ((n >> 2) & 1) : n;
     float pb[NPROJ];
 #pragma unroll
     for (int j = 0; j < NPROJ; ++j) {
@@ -505,17 +539,33 @@ __device__ __forceinline__ void grouped_item(
     for (int rb = 0; rb < NMB; ++rb) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int rr = rb * 16 + 4 * kq + e;
-        if (rr < rows) {
-          if (GU) {
-            const float hv = apply_act(act, acc[rb][cb][0][e] + pb[0],
-                                       acc[rb][cb][NPROJ - 1][e] + pb[NPROJ - 1], alpha, limit);
-            h_out[(int64_t)(r0 + rr) * F + n] = (uint16_t)f32_to_bf16(hv);
-          } else {
-            const int pr = perm[r0 + rr];
-            yp[(int64_t)pr * D + n] = scores[pr] * (acc[rb][cb][0][e] + pb[0]);
+        const int rr = rb * 16 + 4 * kq + e;   // (uniform over each 16-lane row)
+        if (GU) {
+          const float hv = apply_act(act, acc[rb][cb][0][e] + pb[0],
+                                     acc[rb][cb][NPROJ - 1][e] + pb[NPROJ - 1], alpha, limit);
+          const uint32_t hb = f32_to_bf16(hv);
+          if (rr < rows) h_out[(int64_t)(r0 + rr) * F + np] = (uint16_t)hb;
+          if (FUSE) {
+            const float ps = group_sum<16>(bf16_to_f32(hb));
+            if (col == 0) L.part[(wave * CPW + cb) * kTileM + rr] = ps;
           }
+        } else if (rr < rows) {
+          const int pr = perm[r0 + rr];
+          yp[(int64_t)pr * D + n] = scores[pr] * (acc[rb][cb][0][e] + pb[0]);
         }
+      }
+    }
+  }
+  if (FUSE) {
+    __syncthreads();
+#pragma unroll
+    for (int i = tid; i < ROWS * (NB / 64); i += NT) {
+      const int r = i % ROWS, gq = i / ROWS;
+      if (r < rows) {
+        float sm = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) sm += L.part[(gq * 4 + c) * kTileM + r];
+        rs_out[(int64_t)(r0 + r) * (F / 64) + nb0 / 64 + gq] = sm;
       }
     }
   }
@@ -526,7 +576,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
     PoolArgs pa, const uint16_t *__restrict__ aq, const float *__restrict__ ars, int k,
     const int32_t *__restrict__ perm, const int4 *__restrict__ tiles,
     const int32_t *__restrict__ n_tiles, uint16_t *__restrict__ h_out,
-    const float *__restrict__ scores, float *__restrict__ yp, int act, float alpha,
+    float *__restrict__ rs_out, const float *__restrict__ scores, float *__restrict__ yp,
+    int act, float alpha,
     float limit) {
   constexpr int KIN = GU ? D : F, NOUT = GU ? F : D, NPROJ = GU ? 2 : 1;
   constexpr int NBK = NOUT / NB, NP = PBIAS ? 4 : 3;
@@ -536,7 +587,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
   __shared__ uint4 b_l[2 * I::BROWS * 8];
   __shared__ float rs_l[I::NG4 * 4 * kRsPitch];
   __shared__ uint4 sc_l[I::QS ? (I::SQP + 1) / 2 : I::SCP];
-  const GLds L{a_l, b_l, rs_l, sc_l};
+  __shared__ float pt_l[GU && NB % 64 == 0 ? NB / 16 * kTileM : 1];
+  const GLds L{pt_l, a_l, b_l, rs_l, sc_l};
   const int n_items = *n_tiles * NBK;
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
     const int4 tl = tiles[item / NBK];
@@ -555,7 +607,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
     const int nmb = (rows + 15) >> 4;
 #define MOE_GITEM(M)                                                                      \
   grouped_item<M, D, F, PBIAS, NB, WAVES, RA, BR, GU>(pa, aq, ars, k, perm, ref, r0, rows, nb0, h_out, \
-                                              scores, yp, act, alpha, limit, L)
+                                              rs_out, scores, yp, act, alpha, limit, L)
     if (nmb == 1) MOE_GITEM(1);
     else if (nmb == 2) MOE_GITEM(2);
     else if (nmb == 3) MOE_GITEM(3);
@@ -592,16 +644,17 @@ __global__ __launch_bounds__(256) void combine_pairs_kernel(
 template <int D, int F, bool PB, int NBU, int WU, int RU, int BU>
 static void launch_gg(dim3 g, hipStream_t s, const PoolArgs &pa, const uint16_t *xq,
                       const float *rsx, int k, const int32_t *perm, const int4 *tiles,
-                      const int32_t *nt, uint16_t *h, int act, float alpha, float limit) {
+                      const int32_t *nt, uint16_t *h, float *rsh, int act, float alpha,
+                      float limit) {
   hipLaunchKernelGGL((grouped_mm_kernel<D, F, PB, NBU, WU, RU, BU, true>), g, dim3(64 * WU), 0, s, pa,
-                     xq, rsx, k, perm, tiles, nt, h, nullptr, nullptr, act, alpha, limit);
+                     xq, rsx, k, perm, tiles, nt, h, rsh, nullptr, nullptr, act, alpha, limit);
 }
 template <int D, int F, bool PB, int NBD, int WD, int RD, int BD>
 static void launch_gd(dim3 g, hipStream_t s, const PoolArgs &pa, const uint16_t *hq,
                       const float *rsh, const float *sc, const int32_t *perm,
                       const int4 *tiles, const int32_t *nt, float *yp) {
   hipLaunchKernelGGL((grouped_mm_kernel<D, F, PB, NBD, WD, RD, BD, false>), g, dim3(64 * WD), 0, s,
-                     pa, hq, rsh, 1, perm, tiles, nt, nullptr, sc, yp, 0, 0.f, 0.f);
+                     pa, hq, rsh, 1, perm, tiles, nt, nullptr, nullptr, sc, yp, 0, 0.f, 0.f);
 }
 
 // (features per work item, waves, A ring depth in groups, B register sets in
@@ -610,8 +663,8 @@ static void launch_gd(dim3 g, hipStream_t s, const PoolArgs &pa, const uint16_t 
   {D, F, PB, NBU, NBD, &launch_gg<D, F, PB, NBU, WU, RU, BU>,                             \
    &launch_gd<D, F, PB, NBD, WD, RD, BD>}
 static const GroupedLaunch kGroupedTable[] = {
-    MOE_GROUPED_GEOM(2048, 768, false, 64, 4, 8, 1, 64, 4, 4, 1),   // Qwen3-30B-A3B
-    MOE_GROUPED_GEOM(2048, 768, true, 64, 4, 8, 1, 64, 4, 4, 1),
+    MOE_GROUPED_GEOM(2048, 768, false, 64, 4, 8, 1, 128, 8, 4, 1),   // Qwen3-30B-A3B
+    MOE_GROUPED_GEOM(2048, 768, true, 64, 4, 8, 1, 128, 8, 4, 1),
     MOE_GROUPED_GEOM(2880, 2880, true, 96, 6, 4, 2, 192, 6, 4, 2),   // gpt-oss-120b
     MOE_GROUPED_GEOM(2880, 2880, false, 96, 6, 4, 2, 192, 6, 4, 2),
     MOE_GROUPED_GEOM(256, 128, false, 128, 8, 4, 1, 128, 8, 2, 1),   // small test geometry
@@ -675,9 +728,10 @@ void launch_grouped(const GroupedLaunch *G, const PoolArgs &pa, const int32_t *r
                      pa.n_slots, pa.n_records, D, perm, tiles, ntiles, yp);
   launch_prep(x, T, D, xq, rsx, s);
   const int64_t items_up = w.max_tiles * (F / G->nb_up), items_down = w.max_tiles * (D / G->nb_down);
+  const bool fused = G->nb_up % 64 == 0;   // gate/up writes hq and rsh itself
   G->gate_up(dim3((unsigned)std::min<int64_t>(items_up, kGroupedMaxWGs)), s, pa, xq, rsx, k, perm,
-             tiles, ntiles, h, act, alpha, limit);
-  launch_prep(h, P, F, hq, rsh, s);
+             tiles, ntiles, fused ? hq : h, fused ? rsh : nullptr, act, alpha, limit);
+  if (!fused) launch_prep(h, P, F, hq, rsh, s);
   G->down(dim3((unsigned)std::min<int64_t>(items_down, kGroupedMaxWGs)), s, pa, hq, rsh, scores,
           perm, tiles, ntiles, yp);
   const int64_t n4 = (int64_t)T * D / 4;

@@ -70,9 +70,11 @@ constexpr int kGroupedMaxWGs = 2048;    // grid cap; workgroups loop over items
 struct GroupedLaunch {
   int d_model, d_ff, has_bias;
   int nb_up, nb_down;   // output features per work item of gate/up and of down
+  // (with nb_up a multiple of 64 gate/up writes h in the down kernel's input
+  // order with its 64-input row sums, else h as it is)
   void (*gate_up)(dim3, hipStream_t, const PoolArgs &, const uint16_t *, const float *, int,
-                  const int32_t *, const int4 *, const int32_t *, uint16_t *, int, float,
-                  float);
+                  const int32_t *, const int4 *, const int32_t *, uint16_t *, float *, int,
+                  float, float);
   void (*down)(dim3, hipStream_t, const PoolArgs &, const uint16_t *, const float *,
                const float *, const int32_t *, const int4 *, const int32_t *, float *);
 };
