@@ -47,23 +47,34 @@ constexpr int kRsPitch = 80;   // row-sum LDS pitch (floats): 4 groups' rows on 
 // grouping: one workgroup of 1024 threads; hist[] in dynamic LDS spans every
 // valid slot reference, key = ref + n_records in [0, n_slots + n_records).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int y = __shfl_up(v, d, 64);
-    if (lane >= d) v += y;
-  }
+// Inclusive scans on DPP (no LDS round trips): within each 16-lane row
+// (row_shr 1, 2, 4, 8; lanes without a source add 0), and across the wave
+// (then row 0's total into row 1 and row 2's into row 3 by row_bcast:15, rows
+// 0-1's total into rows 2-3 by row_bcast:31).
+__device__ __forceinline__ int row16_incl_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);
+  return v;
+}
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  v = row16_incl_scan(v);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);
   return v;
 }
 
-__global__ __launch_bounds__(1024) void group_pairs_kernel(
+__device__ __forceinline__ void group_pairs_body(
     const int32_t *__restrict__ refs, int n_pairs, int n_slots, int n_records, int D,
     int32_t *__restrict__ perm, int4 *__restrict__ tiles, int32_t *__restrict__ n_tiles,
     float *__restrict__ yp) {
   extern __shared__ int hist[];
   // tiles are listed by size class, largest first (classes 4..1: a tile of
   // r rows is class ceil(r / 16)), so the longest work items start first
-  __shared__ int wsum_p[16], wsum_t[4][16], cbase[5];
+  __shared__ int wsum[5][16];   // per wave: pairs, class-1..4 tiles
+  __shared__ int wpre[5][16];   // exclusive prefixes over the waves
+  __shared__ int cbase[4];      // first tile of each class (class 4 first)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nkeys = n_slots + n_records;
   for (int i = tid; i < nkeys; i += 1024) hist[i] = 0;
@@ -83,46 +94,52 @@ __global__ __launch_bounds__(1024) void group_pairs_kernel(
   const int chunk = (nkeys + 1023) / 1024;
   const int k0 = min(tid * chunk, nkeys), k1 = min(k0 + chunk, nkeys);
   auto tile_class = [](int rows) { return (rows + 15) >> 4; };   // 1..4
-  int sp = 0, st[4] = {0, 0, 0, 0};
+  int st[5] = {0, 0, 0, 0, 0};   // pairs, then tiles of classes 1..4
   for (int i = k0; i < k1; ++i) {
     const int c = hist[i];
-    sp += c;
-    st[3] += c / kTileM;
-    if (c % kTileM) ++st[tile_class(c % kTileM) - 1];
+    const int cl = c % kTileM ? tile_class(c % kTileM) : 0;
+    st[0] += c;
+    st[1] += cl == 1;
+    st[2] += cl == 2;
+    st[3] += cl == 3;
+    st[4] += c / kTileM + (cl == 4);
   }
-  const int ip = wave_incl_scan(sp, lane);
-  int it[4];
+  int it[5];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) it[q] = wave_incl_scan(st[q], lane);
-  if (lane == 63) {
-    wsum_p[wave] = ip;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) wsum_t[q][wave] = it[q];
+  for (int q = 0; q < 5; ++q) {
+    it[q] = wave_incl_scan(st[q]);
+    if (lane == 63) wsum[q][wave] = it[q];
   }
   __syncthreads();
-  if (tid == 0) {   // class bases: class 4 first
-    int b = 0;
-    for (int q = 3; q >= 0; --q) {
-      cbase[q] = b;
-      for (int w = 0; w < 16; ++w) b += wsum_t[q][w];
+  if (wave == 0) {   // the 16 waves' prefixes: one quantity per 16-lane row
+    const int row = lane >> 4, w = lane & 15;
+    __shared__ int ctot[8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int q = h * 4 + row;   // quantities 0-3, then 4
+      const int v = q < 5 ? wsum[q][w] : 0;
+      const int sc = row16_incl_scan(v);
+      if (q < 5) wpre[q][w] = sc - v;
+      if (w == 15) ctot[q] = sc;   // the quantity's total
     }
-    cbase[4] = b;
-    *n_tiles = b;
+    if (lane == 0) {   // class bases, class 4 first
+      const int c1 = ctot[1], c2 = ctot[2], c3 = ctot[3], c4 = ctot[4];
+      cbase[3] = 0;
+      cbase[2] = c4;
+      cbase[1] = c4 + c3;
+      cbase[0] = c4 + c3 + c2;
+      *n_tiles = c4 + c3 + c2 + c1;
+    }
   }
   __syncthreads();
-  int bp = ip - sp, bt[4];
+  int bp = wpre[0][wave] + it[0] - st[0], bt[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) bt[q] = cbase[q] + it[q] - st[q];
-  for (int w = 0; w < wave; ++w) {
-    bp += wsum_p[w];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) bt[q] += wsum_t[q][w];
-  }
+  for (int q = 0; q < 4; ++q) bt[q] = cbase[q] + wpre[q + 1][wave] + it[q + 1] - st[q + 1];
   for (int i = k0; i < k1; ++i) {
     const int c = hist[i];
     hist[i] = bp;   // becomes the scatter cursor of key i
     for (int m = 0; m < c; m += kTileM) {
-      const int rows = min(kTileM, c - m), q = tile_class(rows) - 1;
+      const int rows = min(kTileM, c - m), q = tile_class(rows) - 1;   // bt index
       int t = 0;
 #pragma unroll
       for (int qq = 0; qq < 4; ++qq)   // (registers, not a dynamic index)
@@ -138,6 +155,13 @@ __global__ __launch_bounds__(1024) void group_pairs_kernel(
   }
 }
 
+__global__ __launch_bounds__(1024) void group_pairs_kernel(
+    const int32_t *__restrict__ refs, int n_pairs, int n_slots, int n_records, int D,
+    int32_t *__restrict__ perm, int4 *__restrict__ tiles, int32_t *__restrict__ n_tiles,
+    float *__restrict__ yp) {
+  group_pairs_body(refs, n_pairs, n_slots, n_records, D, perm, tiles, n_tiles, yp);
+}
+
 // B fragment: 8 codes of one weight row as bf16 128+q, x_pairs order.
 __device__ __forceinline__ uint4 b_frag(uint32_t w) {
   uint32_t p[4];
@@ -151,13 +175,12 @@ __device__ __forceinline__ uint4 b_frag(uint32_t w) {
 // 64-input row sums, once per call: one thread per piece, the 8 pieces of a
 // group in 8 consecutive lanes (rs: [rows][K / 64] fp32).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void grouped_prep_kernel(const uint16_t *__restrict__ src,
-                                                           int64_t rows, int K,
-                                                           uint16_t *__restrict__ dst,
-                                                           float *__restrict__ rs) {
-  // (32-bit index arithmetic: the host launches at most 2^30 pieces at a time)
+// piece i of `rows` rows of K inputs (32-bit index arithmetic: the host
+// passes at most 2^30 pieces at a time)
+__device__ __forceinline__ void prep_piece(int i, const uint16_t *__restrict__ src, int64_t rows,
+                                           int K, uint16_t *__restrict__ dst,
+                                           float *__restrict__ rs) {
   const int ppr = K / 8;
-  const int i = blockIdx.x * 256 + threadIdx.x;
   const bool ok = i < (int)(rows * ppr);
   const int r = ok ? i / ppr : 0;
   const int pc = ok ? i - r * ppr : 0;
@@ -174,6 +197,26 @@ __global__ __launch_bounds__(256) void grouped_prep_kernel(const uint16_t *__res
     *reinterpret_cast<uint4 *>(dst + (int64_t)r * K + pc * 8) = make_uint4(out[0], out[1], out[2], out[3]);
     if ((pc & 7) == 0) rs[(int64_t)r * (K / 64) + pc / 8] = sm;
   }
+}
+
+__global__ __launch_bounds__(256) void grouped_prep_kernel(const uint16_t *__restrict__ src,
+                                                           int64_t rows, int K,
+                                                           uint16_t *__restrict__ dst,
+                                                           float *__restrict__ rs) {
+  prep_piece(blockIdx.x * 256 + threadIdx.x, src, rows, K, dst, rs);
+}
+
+// The grouping (workgroup 0) and the token rows' prep (the other workgroups)
+// in one launch: they are independent, so the prep runs beside the grouping.
+__global__ __launch_bounds__(1024) void group_prep_kernel(
+    const int32_t *__restrict__ refs, int n_pairs, int n_slots, int n_records, int D,
+    int32_t *__restrict__ perm, int4 *__restrict__ tiles, int32_t *__restrict__ n_tiles,
+    float *__restrict__ yp, const uint16_t *__restrict__ x, int64_t T, uint16_t *__restrict__ xq,
+    float *__restrict__ rsx) {
+  if (blockIdx.x == 0)
+    group_pairs_body(refs, n_pairs, n_slots, n_records, D, perm, tiles, n_tiles, yp);
+  else
+    prep_piece((blockIdx.x - 1) * 1024 + threadIdx.x, x, T, D, xq, rsx);
 }
 
 // ---------------------------------------------------------------------------
@@ -724,9 +767,16 @@ void launch_grouped(const GroupedLaunch *G, const PoolArgs &pa, const int32_t *r
   uint16_t *hq = reinterpret_cast<uint16_t *>(ws + w.off_hq);
   float *rsh = reinterpret_cast<float *>(ws + w.off_rsh);
   const int nkeys = pa.n_slots + pa.n_records;
-  hipLaunchKernelGGL(group_pairs_kernel, dim3(1), dim3(1024), (size_t)nkeys * 4, s, refs, P,
-                     pa.n_slots, pa.n_records, D, perm, tiles, ntiles, yp);
-  launch_prep(x, T, D, xq, rsx, s);
+  const int64_t xpieces = (int64_t)T * (D / 8);
+  if (xpieces < ((int64_t)1 << 30)) {   // grouping and x prep in one launch
+    hipLaunchKernelGGL(group_prep_kernel, dim3((unsigned)(1 + (xpieces + 1023) / 1024)), dim3(1024),
+                       (size_t)nkeys * 4, s, refs, P, pa.n_slots, pa.n_records, D, perm, tiles,
+                       ntiles, yp, x, (int64_t)T, xq, rsx);
+  } else {
+    hipLaunchKernelGGL(group_pairs_kernel, dim3(1), dim3(1024), (size_t)nkeys * 4, s, refs, P,
+                       pa.n_slots, pa.n_records, D, perm, tiles, ntiles, yp);
+    launch_prep(x, T, D, xq, rsx, s);
+  }
   const int64_t items_up = w.max_tiles * (F / G->nb_up), items_down = w.max_tiles * (D / G->nb_down);
   const bool fused = G->nb_up % 64 == 0;   // gate/up writes hq and rsh itself
   G->gate_up(dim3((unsigned)std::min<int64_t>(items_up, kGroupedMaxWGs)), s, pa, xq, rsx, k, perm,
