@@ -227,41 +227,38 @@ __global__ __launch_bounds__(1024) void group_prep_kernel(
 // the NMB 16-row blocks the tile fills (a template parameter: no branches
 // around the MFMAs).
 //
-// Operands per 64-input quant group g:
-//  * A: the group's rows x 8 pieces, loaded RA - 1 groups ahead into a
-//    register ring and copied to LDS before the group's barrier: row-major,
-//    piece p of row r at r * 8 + (p ^ (r & 7)), so each 8-lane run of the
-//    copy writes one whole row (no bank conflict) and the MFMA reads of a
-//    piece across 16 rows fall on distinct banks.
-//  * B: the weights' codes of 4 groups at a time (a "quad", 128 bytes of
-//    every weight row: whole cache lines, 8 lanes per row), loaded BR quads
-//    ahead into registers and copied to LDS at the quad's first group.  Row
-//    layout in LDS: 8 chunks of 16 bytes, chunk c stored at c ^ (row & 7)
-//    with its two 8-byte halves swapped when row & 8, so the 16 rows read by
-//    one B-fragment load fall on distinct banks.  Each lane then reads its
-//    two code words (8 bytes) per group.
-// Every thread issues the same loads on every path (rows past the tile,
-// chunks past the row and refills past the end are either clamped to a
-// valid address and never used, or decided at compile time), so the
-// compiler's counter waits ask for exactly the data in hand while later
-// loads stay in flight.  The item's scales, biases and row sums are staged
-// in LDS once: scales quad-major (each lane reads its row's 4 scales of a
-// quad as 8 contiguous bytes, the 16 rows of a fragment side by side), row
-// sums at a pitch of 80 floats (the 4 groups of one bias MFMA on distinct
-// banks).  Each group accumulates into a fresh 16x16 block (2 MFMAs over
-// the bf16 128+q codes), folded into the output by S; the bias term
-// sum_g rowsum[g] * (B - 128 S) runs on fp32 MFMAs (K = 4 groups) at the end.
+// The inputs are processed a quad (4 quant groups of 64 inputs) at a time.
+// A quad's operands sit in LDS while the workgroup computes its 4 groups
+// with no barrier in between; the next quad's operands wait in registers
+// (their loads issued a quad earlier) and go to LDS between two barriers at
+// the quad's end, when the loads of the quad after it are issued.
+//  * A: the token rows' 8-input pieces, row-major per group, piece p of row r
+//    at r * 8 + (p ^ (r & 7)): each 8-lane run of the copy writes one whole
+//    row (no bank conflict) and the MFMA reads of a piece across 16 rows fall
+//    on distinct banks.
+//  * B: 128 bytes of every weight row per quad (whole cache lines, 8 lanes
+//    per row); in LDS 8 chunks of 16 bytes, chunk c at c ^ ((row >> 1) & 7),
+//    so the 32 lanes of one 8-byte fragment read (16 rows x 2 halves) fall on
+//    distinct banks.  Each lane reads its two code words (8 bytes) per group.
+// Every thread issues the same loads on every path (rows past the tile and
+// chunks past the row are clamped to a valid address and never used; the
+// last quads are unrolled), so the compiler's counter waits ask for exactly
+// the data in hand.  The item's scales, biases and row sums are staged in
+// LDS once: scales quad-major (each lane reads its row's 4 scales of a quad
+// as 8 contiguous bytes, the 16 rows of a fragment side by side), row sums at
+// a pitch of 80 floats (the 4 groups of one bias MFMA on distinct banks).
+// Each group accumulates into a fresh 16x16 block (2 MFMAs over the bf16
+// 128+q codes), folded into the output by S; the bias term
+// sum_g rowsum[g] * (B - 128 S) runs on fp32 MFMAs (K = 4 groups) per quad.
 // Rows past the tile compute garbage from a copy of a real row, which no
 // output row depends on (MFMA rows are independent) and nothing stores.
 // ---------------------------------------------------------------------------
-template <int KIN, int NB, int WAVES, int NPROJ, int RA_, int BR_>
+template <int KIN, int NB, int WAVES, int NPROJ>
 struct GItem {
   static constexpr int NT = 64 * WAVES;
   static constexpr int NG = KIN / 64;                  // quant groups along the inputs
   static constexpr int NQ = (NG + 3) / 4;              // quads (B staging units)
   static constexpr int NG4 = NQ;                       // bias MFMAs, 4 groups each
-  static constexpr int RA = RA_;                       // A ring slots (groups)
-  static constexpr int BR = BR_;                       // B register sets (quads)
   static constexpr int CPW = NB / 16 / WAVES;          // column blocks per wave
   static constexpr int SPT = (kTileM * 8 + NT - 1) / NT;   // A pieces per thread and group
   static constexpr int BROWS = NPROJ * NB;             // weight rows of the item
@@ -278,39 +275,29 @@ struct GItem {
   static constexpr int RSW = (NG4 * 4 + WAVES - 1) / WAVES;   // row-sum groups per thread
   static_assert(KIN % 64 == 0 && NB % (16 * WAVES) == 0 && CPW >= 1, "feature split");
   static_assert(SCB % 16 == 0 && NT % 8 == 0 && (BROWS * 8) % NT == 0, "staging");
-  static_assert(8 % RA == 0 && RA >= 2 && (BR == 1 || BR == 2), "rings within an 8-group step");
-  // A refill at group g loads g + RA - 1; B refill at quad q loads q + BR.
-  // Steps of 8 groups [8t, 8t + 8) whose refills are all in range run as a
-  // loop (MAIN of them); the remaining groups are unrolled.
-  static constexpr bool step_full(int t) {
-    return 8 * t + 7 + RA - 1 < NG && 2 * t + 1 + BR < NQ;
-  }
-  static constexpr int main_steps() {
-    int t = 0;
-    while (step_full(t)) ++t;
-    return t;
-  }
-  static constexpr int MAIN = main_steps();
+  // quads [0, QMAIN) refill the registers with quad q + 2 (a loop); the last
+  // two quads are unrolled
+  static constexpr int QMAIN = NQ >= 2 ? NQ - 2 : 0;
 };
 
 struct GLds {   // (one layout for every instantiation; sized by the caller)
   float *part;             // gate/up with the fused input prep: [NB / 16][64] row partial sums
-  uint4 (*a)[kTileM * 8];  // [2][row * 8 + (piece ^ (row & 7))]
+  uint4 (*a)[kTileM * 8];  // [4 groups][row * 8 + (piece ^ (row & 7))]
   uint4 *b;                // [2][BROWS][8]: two quads of codes
   float *rs;               // [NG4 * 4][kRsPitch]: 64-input row sums (row < 64), zero past NG
   uint4 *sc;
 };
 
-template <int NMB, int D, int F, bool PBIAS, int NB, int WAVES, int RA_, int BR_, bool GU>
+template <int NMB, int D, int F, bool PBIAS, int NB, int WAVES, bool GU>
 __device__ __forceinline__ void grouped_item(
     const PoolArgs &pa, const uint16_t *__restrict__ aq, const float *__restrict__ ars, int k,
     const int32_t *__restrict__ perm, int ref, int r0, int rows, int nb0,
     uint16_t *__restrict__ h_out, float *__restrict__ rs_out, const float *__restrict__ scores,
     float *__restrict__ yp, int act, float alpha, float limit, const GLds &L) {
   constexpr int KIN = GU ? D : F, NPROJ = GU ? 2 : 1;
-  using I = GItem<KIN, NB, WAVES, NPROJ, RA_, BR_>;
+  using I = GItem<KIN, NB, WAVES, NPROJ>;
   constexpr int NG = I::NG, NQ = I::NQ, CPW = I::CPW, NT = I::NT, SPT = I::SPT;
-  constexpr int RA = I::RA, BR = I::BR, BPT = I::BPT;
+  constexpr int BPT = I::BPT;
   constexpr int NP = PBIAS ? 4 : 3, SCH = I::SCB / 2;   // halfwords per scale array block
   constexpr int ROWS = NMB * 16;                        // staged rows
   constexpr int RB = KIN / 2;                           // bytes per weight row
@@ -346,13 +333,13 @@ __device__ __forceinline__ void grouped_item(
   // this thread's B pieces: piece p = tid + NT * i is chunk p % 8 of item
   // weight row p / 8 (rows [0, NB) the first projection, then the second)
   const char *bsrc[BPT];
-  uint32_t bdst[BPT];   // LDS byte offset of the piece's low half in a quad buffer
+  uint32_t bdst[BPT];   // LDS byte offset of the piece in the quad buffer
 #pragma unroll
   for (int i = 0; i < BPT; ++i) {
     const int p = tid + NT * i, row = p >> 3, c = p & 7;
     const int j = row / NB, fl = row % NB;
     bsrc[i] = w[NPROJ > 1 ? j : 0] + (int64_t)(nb0 + fl) * RB + c * 16;
-    bdst[i] = (uint32_t)(row * 128 + ((c ^ (row & 7)) << 4) + ((row & 8) ? 8 : 0));
+    bdst[i] = (uint32_t)(row * 128 + ((c ^ ((row >> 1) & 7)) << 4));
   }
   auto load_b = [&](int q, uint4 (&v)[BPT]) {
 #pragma unroll
@@ -367,27 +354,21 @@ __device__ __forceinline__ void grouped_item(
   auto store_b = [&](int buf, const uint4 (&v)[BPT]) {
     char *base = reinterpret_cast<char *>(L.b + buf * I::BROWS * 8);
 #pragma unroll
-    for (int i = 0; i < BPT; ++i) {
-      // one 16-byte write per piece, halves swapped for rows with row & 8
-      const bool sw = (bdst[i] & 8) != 0;
-      const uint32_t x = v[i].x, y = v[i].y, z = v[i].z, w = v[i].w;
-      *reinterpret_cast<uint4 *>(base + (bdst[i] & ~8u)) =
-          make_uint4(sw ? z : x, sw ? w : y, sw ? x : z, sw ? y : w);
-    }
+    for (int i = 0; i < BPT; ++i) *reinterpret_cast<uint4 *>(base + bdst[i]) = v[i];
   };
   // this lane's B fragment rows: feature col of column block cb, projection j
   uint32_t bfr[NPROJ][CPW];   // LDS byte offset of the row in a quad buffer
-  uint32_t bx[NPROJ][CPW];    // its chunk swizzle (row & 7) and half swap (row & 8)
+  uint32_t bx[NPROJ][CPW];    // its chunk swizzle ((row >> 1) & 7), as a byte offset
 #pragma unroll
   for (int j = 0; j < NPROJ; ++j)
 #pragma unroll
     for (int cb = 0; cb < CPW; ++cb) {
       const int row = j * NB + (wave * CPW + cb) * 16 + col;
       bfr[j][cb] = row * 128;
-      bx[j][cb] = ((row & 7) << 4) | ((row & 8) ? 8 : 0);
+      bx[j][cb] = ((row >> 1) & 7) << 4;
     }
   // the item's scales and biases (each array's NB rows are one contiguous
-  // block) and row sums, loaded ahead of the rings and written to LDS after
+  // block) and row sums, loaded ahead of the first quad and written to LDS after
   constexpr bool QS = I::QS;
   constexpr int SCN = QS ? I::SQW : I::SCW;
   uint4 scv[QS ? 1 : I::SCW];
@@ -410,14 +391,32 @@ __device__ __forceinline__ void grouped_item(
 #pragma unroll
     for (int j = 0; j < I::RSW; ++j) rsv[j] = gload4f(rrow + min(wave + WAVES * j, NG - 1));
   }
-  uint4 breg[BR][BPT];
+  // one quad of token-row pieces and codes in registers at a time
+  uint4 breg[BPT];
+  uint4 areg[4][SPT];
+  auto load_quad = [&](int q, int ng) {   // ng: the quad's groups (a constant)
 #pragma unroll
-  for (int q = 0; q < BR; ++q)
-    if (q < NQ) load_b(q, breg[q]);
-  uint4 areg[RA][SPT];
+    for (int gi = 0; gi < 4; ++gi)
+      if (gi < ng) load_a(4 * q + gi, areg[gi]);
+    load_b(q, breg);
+  };
+  auto store_quad = [&](int ng) {
 #pragma unroll
-  for (int i = 0; i + 1 < RA; ++i)
-    if (i < NG) load_a(i, areg[i]);
+    for (int gi = 0; gi < 4; ++gi) {
+      if (gi >= ng) continue;
+#pragma unroll
+      for (int j = 0; j < SPT; ++j) {
+        const int sl = tid + NT * j;
+        if (sl < ROWS * 8) {   // uniform per wave
+          const int r = sl >> 3, p = sl & 7;
+          L.a[gi][r * 8 + (p ^ (r & 7))] = areg[gi][j];
+        }
+      }
+    }
+    store_b(0, breg);
+  };
+  constexpr int NGL = NG - 4 * (NQ - 1);   // groups of the last quad
+  load_quad(0, NQ > 1 ? 4 : NGL);
 #pragma unroll
   for (int j = 0; j < SCN; ++j) {
     if (QS) {
@@ -439,6 +438,9 @@ __device__ __forceinline__ void grouped_item(
     for (int cb = 0; cb < CPW; ++cb)
 #pragma unroll
       for (int j = 0; j < NPROJ; ++j) acc[rb][cb][j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+  store_quad(NQ > 1 ? 4 : NGL);
+  if (NQ > 1) load_quad(1, NQ > 2 ? 4 : NGL);
+  __syncthreads();
   // with quad-major scales each lane reads its row's scales 4 groups at a
   // time (8 bytes at the quad's first group)
   const uint2 *scq = reinterpret_cast<const uint2 *>(L.sc);
@@ -482,27 +484,9 @@ __device__ __forceinline__ void grouped_item(
         }
     }
   };
-  // one group (gi: g mod 8, known at compile time in every unrolled copy;
-  // the refill and bias flags likewise)
-  auto group = [&](int g, int gi, bool a_refill, bool b_refill, bool bias_now) {
-    if (gi % 4 == 0) {   // a quad starts: its codes to LDS, refill their registers
-      const int q = g >> 2, bs = (gi / 4) % BR;
-      store_b(q & 1, breg[bs]);
-      if (b_refill) load_b(q + BR, breg[bs]);
-    }
-    uint4 *al = L.a[g & 1];
-    const int s = gi % RA;
-#pragma unroll
-    for (int j = 0; j < SPT; ++j) {
-      const int sl = tid + NT * j;
-      if (sl < ROWS * 8) {   // uniform per wave
-        const int r = sl >> 3, p = sl & 7;
-        al[r * 8 + (p ^ (r & 7))] = areg[s][j];
-      }
-    }
-    __syncthreads();
-    if (a_refill) load_a(g + RA - 1, areg[(s + RA - 1) % RA]);
-    if (QS && gi % 4 == 0) {   // the quad's scales, 4 halfwords per lane and row
+  // one group of the quad in LDS (gi: its index in the quad, a constant)
+  auto group = [&](int g, int gi) {
+    if (QS && gi == 0) {   // the quad's scales, 4 halfwords per lane and row
 #pragma unroll
       for (int j = 0; j < NPROJ; ++j)
 #pragma unroll
@@ -511,8 +495,9 @@ __device__ __forceinline__ void grouped_item(
           s4[j][cb] = scq[((2 * j) * NQ + (g >> 2)) * NB + nl];
         }
     }
-    const char *bq = reinterpret_cast<const char *>(L.b + ((g >> 2) & 1) * I::BROWS * 8);
-    const uint32_t cpos = (uint32_t)((gi % 4) * 32 + kq * 8);   // logical chunk and half
+    const uint4 *al = L.a[gi];
+    const char *bq = reinterpret_cast<const char *>(L.b);
+    const uint32_t cpos = (uint32_t)(gi * 32 + kq * 8);   // logical chunk and half
     uint4 b0[NPROJ][CPW], b1[NPROJ][CPW];
     float S[NPROJ][CPW];
 #pragma unroll
@@ -523,7 +508,7 @@ __device__ __forceinline__ void grouped_item(
         b0[j][cb] = b_frag(cw.x);
         b1[j][cb] = b_frag(cw.y);
         if (QS) {
-          const uint32_t h = (gi % 4) < 2 ? s4[j][cb].x : s4[j][cb].y;
+          const uint32_t h = gi < 2 ? s4[j][cb].x : s4[j][cb].y;
           S[j][cb] = __uint_as_float((gi & 1) ? (h & 0xffff0000u) : (h << 16));
         } else {
           const int nl = (wave * CPW + cb) * 16 + col;
@@ -549,15 +534,25 @@ __device__ __forceinline__ void grouped_item(
           asm volatile("" ::"v"(c0), "v"(acc[rb][cb][j]));
         }
     }
-    if (bias_now) bias_step(g >> 2, s4);   // the quad's last group
   };
-  for (int g0 = 0; g0 < I::MAIN * 8; g0 += 8) {
+  // one quad: its groups from LDS, its bias term; then (all waves done with
+  // the quad) the next quad's operands from registers to LDS and the loads of
+  // the one after
+  auto quad = [&](int q, int ng, bool next, int ng_next, bool refill, int ng_refill) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) group(g0 + i, i, true, true, i % 4 == 3);
-  }
-#pragma unroll
-  for (int g = I::MAIN * 8; g < NG; ++g)
-    group(g, g % 8, g + RA - 1 < NG, (g >> 2) + BR < NQ, g % 4 == 3 || g == NG - 1);
+    for (int gi = 0; gi < 4; ++gi)
+      if (gi < ng) group(4 * q + gi, gi);
+    bias_step(q, s4);
+    if (next) {
+      __syncthreads();
+      store_quad(ng_next);
+      if (refill) load_quad(q + 2, ng_refill);
+      __syncthreads();
+    }
+  };
+  for (int q = 0; q < I::QMAIN; ++q) quad(q, 4, true, 4, true, q + 2 < NQ - 1 ? 4 : NGL);
+  if (NQ >= 2) quad(NQ - 2, 4, true, NGL, false, 0);
+  quad(NQ - 1, NGL, false, 0, false, 0);
   // epilogue.  Gate/up with NB a multiple of 64 also does the down kernel's
   // input prep: h goes out in x_pairs order (feature f of an 8-feature piece
   // at 2 * (f % 4) + f / 4) with the sums of its bf16 values over each
@@ -614,7 +609,7 @@ __device__ __forceinline__ void grouped_item(
   }
 }
 
-template <int D, int F, bool PBIAS, int NB, int WAVES, int RA, int BR, bool GU>
+template <int D, int F, bool PBIAS, int NB, int WAVES, bool GU>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2))) void grouped_mm_kernel(
     PoolArgs pa, const uint16_t *__restrict__ aq, const float *__restrict__ ars, int k,
     const int32_t *__restrict__ perm, const int4 *__restrict__ tiles,
@@ -624,10 +619,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
     float limit) {
   constexpr int KIN = GU ? D : F, NOUT = GU ? F : D, NPROJ = GU ? 2 : 1;
   constexpr int NBK = NOUT / NB, NP = PBIAS ? 4 : 3;
-  using I = GItem<KIN, NB, WAVES, NPROJ, RA, BR>;
+  using I = GItem<KIN, NB, WAVES, NPROJ>;
   static_assert(NOUT % NB == 0, "whole feature blocks");
-  __shared__ uint4 a_l[2][kTileM * 8];
-  __shared__ uint4 b_l[2 * I::BROWS * 8];
+  __shared__ uint4 a_l[4][kTileM * 8];
+  __shared__ uint4 b_l[I::BROWS * 8];
   __shared__ float rs_l[I::NG4 * 4 * kRsPitch];
   __shared__ uint4 sc_l[I::QS ? (I::SQP + 1) / 2 : I::SCP];
   __shared__ float pt_l[GU && NB % 64 == 0 ? NB / 16 * kTileM : 1];
@@ -649,7 +644,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
     }
     const int nmb = (rows + 15) >> 4;
 #define MOE_GITEM(M)                                                                      \
-  grouped_item<M, D, F, PBIAS, NB, WAVES, RA, BR, GU>(pa, aq, ars, k, perm, ref, r0, rows, nb0, h_out, \
+  grouped_item<M, D, F, PBIAS, NB, WAVES, GU>(pa, aq, ars, k, perm, ref, r0, rows, nb0, h_out, \
                                               rs_out, scores, yp, act, alpha, limit, L)
     if (nmb == 1) MOE_GITEM(1);
     else if (nmb == 2) MOE_GITEM(2);
@@ -684,34 +679,32 @@ __global__ __launch_bounds__(256) void combine_pairs_kernel(
 }
 
 // ---------------------------------------------------------------------------
-template <int D, int F, bool PB, int NBU, int WU, int RU, int BU>
+template <int D, int F, bool PB, int NBU, int WU>
 static void launch_gg(dim3 g, hipStream_t s, const PoolArgs &pa, const uint16_t *xq,
                       const float *rsx, int k, const int32_t *perm, const int4 *tiles,
                       const int32_t *nt, uint16_t *h, float *rsh, int act, float alpha,
                       float limit) {
-  hipLaunchKernelGGL((grouped_mm_kernel<D, F, PB, NBU, WU, RU, BU, true>), g, dim3(64 * WU), 0, s, pa,
+  hipLaunchKernelGGL((grouped_mm_kernel<D, F, PB, NBU, WU, true>), g, dim3(64 * WU), 0, s, pa,
                      xq, rsx, k, perm, tiles, nt, h, rsh, nullptr, nullptr, act, alpha, limit);
 }
-template <int D, int F, bool PB, int NBD, int WD, int RD, int BD>
+template <int D, int F, bool PB, int NBD, int WD>
 static void launch_gd(dim3 g, hipStream_t s, const PoolArgs &pa, const uint16_t *hq,
                       const float *rsh, const float *sc, const int32_t *perm,
                       const int4 *tiles, const int32_t *nt, float *yp) {
-  hipLaunchKernelGGL((grouped_mm_kernel<D, F, PB, NBD, WD, RD, BD, false>), g, dim3(64 * WD), 0, s,
+  hipLaunchKernelGGL((grouped_mm_kernel<D, F, PB, NBD, WD, false>), g, dim3(64 * WD), 0, s,
                      pa, hq, rsh, 1, perm, tiles, nt, nullptr, nullptr, sc, yp, 0, 0.f, 0.f);
 }
 
-// (features per work item, waves, A ring depth in groups, B register sets in
-// quads) of gate/up and of down per geometry
-#define MOE_GROUPED_GEOM(D, F, PB, NBU, WU, RU, BU, NBD, WD, RD, BD)                    \
-  {D, F, PB, NBU, NBD, &launch_gg<D, F, PB, NBU, WU, RU, BU>,                             \
-   &launch_gd<D, F, PB, NBD, WD, RD, BD>}
+// (features per work item, waves) of gate/up and of down per geometry
+#define MOE_GROUPED_GEOM(D, F, PB, NBU, WU, NBD, WD)                                     \
+  {D, F, PB, NBU, NBD, &launch_gg<D, F, PB, NBU, WU>, &launch_gd<D, F, PB, NBD, WD>}
 static const GroupedLaunch kGroupedTable[] = {
-    MOE_GROUPED_GEOM(2048, 768, false, 64, 4, 8, 1, 128, 8, 4, 1),   // Qwen3-30B-A3B
-    MOE_GROUPED_GEOM(2048, 768, true, 64, 4, 8, 1, 128, 8, 4, 1),
-    MOE_GROUPED_GEOM(2880, 2880, true, 96, 6, 4, 2, 192, 6, 4, 2),   // gpt-oss-120b
-    MOE_GROUPED_GEOM(2880, 2880, false, 96, 6, 4, 2, 192, 6, 4, 2),
-    MOE_GROUPED_GEOM(256, 128, false, 128, 8, 4, 1, 128, 8, 2, 1),   // small test geometry
-    MOE_GROUPED_GEOM(256, 128, true, 128, 8, 4, 1, 128, 8, 2, 1),
+    MOE_GROUPED_GEOM(2048, 768, false, 64, 4, 128, 8),   // Qwen3-30B-A3B
+    MOE_GROUPED_GEOM(2048, 768, true, 64, 4, 128, 8),
+    MOE_GROUPED_GEOM(2880, 2880, true, 96, 6, 192, 6),   // gpt-oss-120b
+    MOE_GROUPED_GEOM(2880, 2880, false, 96, 6, 192, 6),
+    MOE_GROUPED_GEOM(256, 128, false, 128, 8, 128, 8),   // small test geometry
+    MOE_GROUPED_GEOM(256, 128, true, 128, 8, 128, 8),
 };
 
 const GroupedLaunch *find_grouped(int d_model, int d_ff, int has_bias) {
