@@ -282,8 +282,10 @@ struct GItem {
 
 struct GLds {   // (one layout for every instantiation; sized by the caller)
   float *part;             // gate/up with the fused input prep: [NB / 16][64] row partial sums
+  int *rperm;              // down: the tile rows' pair ids [64] ...
+  float *rsc;              // ... and their scores [64]
   uint4 (*a)[kTileM * 8];  // [4 groups][row * 8 + (piece ^ (row & 7))]
-  uint4 *b;                // [2][BROWS][8]: two quads of codes
+  uint4 *b;                // [BROWS][8]: one quad of codes
   float *rs;               // [NG4 * 4][kRsPitch]: 64-input row sums (row < 64), zero past NG
   uint4 *sc;
 };
@@ -417,6 +419,14 @@ __device__ __forceinline__ void grouped_item(
   };
   constexpr int NGL = NG - 4 * (NQ - 1);   // groups of the last quad
   load_quad(0, NQ > 1 ? 4 : NGL);
+  // down: the pair id and score of tile row `lane` for the epilogue (every
+  // wave loads them, wave 0 keeps them: no branch around the loads)
+  int my_pr = 0;
+  float my_sc = 0.f;
+  if (!GU) {
+    my_pr = gload4i(perm + r0 + min(lane, rows - 1));
+    my_sc = gload4f(scores + my_pr);
+  }
 #pragma unroll
   for (int j = 0; j < SCN; ++j) {
     if (QS) {
@@ -439,6 +449,10 @@ __device__ __forceinline__ void grouped_item(
 #pragma unroll
       for (int j = 0; j < NPROJ; ++j) acc[rb][cb][j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
   store_quad(NQ > 1 ? 4 : NGL);
+  if (!GU && wave == 0) {
+    L.rperm[lane] = my_pr;
+    L.rsc[lane] = my_sc;
+  }
   if (NQ > 1) load_quad(1, NQ > 2 ? 4 : NGL);
   __syncthreads();
   // with quad-major scales each lane reads its row's scales 4 groups at a
@@ -553,16 +567,22 @@ __device__ __forceinline__ void grouped_item(
   for (int q = 0; q < I::QMAIN; ++q) quad(q, 4, true, 4, true, q + 2 < NQ - 1 ? 4 : NGL);
   if (NQ >= 2) quad(NQ - 2, 4, true, NGL, false, 0);
   quad(NQ - 1, NGL, false, 0, false, 0);
-  // epilogue.  Gate/up with NB a multiple of 64 also does the down kernel's
-  // input prep: h goes out in x_pairs order (feature f of an 8-feature piece
-  // at 2 * (f % 4) + f / 4) with the sums of its bf16 values over each
-  // 64-feature group (16 features per 16-lane row, then 4 column blocks in
-  // order through LDS).
+  // epilogue.  The item's output tile goes through LDS (the quad buffers,
+  // free once every wave is past the last quad) and out as whole rows, 16
+  // bytes per lane.  Gate/up with NB a multiple of 64 also does the down
+  // kernel's input prep: h goes out in x_pairs order (feature f of an
+  // 8-feature piece at 2 * (f % 4) + f / 4) with the sums of its bf16 values
+  // over each 64-feature group (16 features per 16-lane row, then 4 column
+  // blocks in order through LDS).  Down scales each row by its score.
   constexpr bool FUSE = GU && NB % 64 == 0;
+  constexpr int OB = GU ? 2 : 4;                          // output bytes per element
+  constexpr bool STAGE = ROWS * NB * OB <= (int)(4 * kTileM * 8 * sizeof(uint4));
+  __syncthreads();
+  char *tile = reinterpret_cast<char *>(L.a[0]);
 #pragma unroll
   for (int cb = 0; cb < CPW; ++cb) {
-    const int n = nb0 + (wave * CPW + cb) * 16 + col;
-    const int np = FUSE ? (n & ~7) + ((n & 3) << 1) + ((n >> 2) & 1) : n;
+    const int nl = (wave * CPW + cb) * 16 + col, n = nb0 + nl;
+    const int npl = FUSE ? (nl & ~7) + ((nl & 3) << 1) + ((nl >> 2) & 1) : nl;
     float pb[NPROJ];
 #pragma unroll
     for (int j = 0; j < NPROJ; ++j) {
@@ -578,24 +598,51 @@ __device__ __forceinline__ void grouped_item(
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int rr = rb * 16 + 4 * kq + e;   // (uniform over each 16-lane row)
+        // staged tile: row rr, element npl ^ (16 * ((rr >> 2) & 3)) (the 4
+        // rows of one store fall on distinct banks)
+        const int ec = npl ^ (((rr >> 2) & 3) << 4);
         if (GU) {
           const float hv = apply_act(act, acc[rb][cb][0][e] + pb[0],
                                      acc[rb][cb][NPROJ - 1][e] + pb[NPROJ - 1], alpha, limit);
           const uint32_t hb = f32_to_bf16(hv);
-          if (rr < rows) h_out[(int64_t)(r0 + rr) * F + np] = (uint16_t)hb;
+          if (STAGE)
+            reinterpret_cast<uint16_t *>(tile)[rr * NB + ec] = (uint16_t)hb;
+          else if (rr < rows)
+            h_out[(int64_t)(r0 + rr) * F + nb0 + npl] = (uint16_t)hb;
           if (FUSE) {
             const float ps = group_sum<16>(bf16_to_f32(hb));
             if (col == 0) L.part[(wave * CPW + cb) * kTileM + rr] = ps;
           }
-        } else if (rr < rows) {
-          const int pr = perm[r0 + rr];
-          yp[(int64_t)pr * D + n] = scores[pr] * (acc[rb][cb][0][e] + pb[0]);
+        } else {
+          const float v = acc[rb][cb][0][e] + pb[0];
+          if (STAGE) {
+            reinterpret_cast<float *>(tile)[rr * NB + ec] = L.rsc[rr] * v;
+          } else if (rr < rows) {
+            const int pr = L.rperm[rr];
+            yp[(int64_t)pr * D + n] = L.rsc[rr] * v;
+          }
         }
       }
     }
   }
+  __syncthreads();
+  if (STAGE) {   // whole rows out, 16 bytes per lane
+    constexpr int CPR = NB * OB / 16;                     // 16-byte chunks per row
+    constexpr int EPC = 16 / OB;                          // elements per chunk
+#pragma unroll 1
+    for (int it = 0; it < (ROWS * CPR + NT - 1) / NT; ++it) {
+      const int i = tid + NT * it, r = i / CPR, c = i % CPR;
+      if (i < ROWS * CPR && r < rows) {
+        const int ec = (c * EPC) ^ (((r >> 2) & 3) << 4);
+        const uint4 v = *reinterpret_cast<const uint4 *>(tile + (r * NB + ec) * OB);
+        if (GU)
+          *reinterpret_cast<uint4 *>(h_out + (int64_t)(r0 + r) * F + nb0 + c * EPC) = v;
+        else
+          *reinterpret_cast<uint4 *>(yp + (int64_t)L.rperm[r] * D + nb0 + c * EPC) = v;
+      }
+    }
+  }
   if (FUSE) {
-    __syncthreads();
 #pragma unroll
     for (int i = tid; i < ROWS * (NB / 64); i += NT) {
       const int r = i % ROWS, gq = i / ROWS;
@@ -610,7 +657,7 @@ __device__ __forceinline__ void grouped_item(
 }
 
 template <int D, int F, bool PBIAS, int NB, int WAVES, bool GU>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2))) void grouped_mm_kernel(
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(WAVES == 8 && !GU ? 4 : 2))) void grouped_mm_kernel(
     PoolArgs pa, const uint16_t *__restrict__ aq, const float *__restrict__ ars, int k,
     const int32_t *__restrict__ perm, const int4 *__restrict__ tiles,
     const int32_t *__restrict__ n_tiles, uint16_t *__restrict__ h_out,
@@ -626,7 +673,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2)))
   __shared__ float rs_l[I::NG4 * 4 * kRsPitch];
   __shared__ uint4 sc_l[I::QS ? (I::SQP + 1) / 2 : I::SCP];
   __shared__ float pt_l[GU && NB % 64 == 0 ? NB / 16 * kTileM : 1];
-  const GLds L{pt_l, a_l, b_l, rs_l, sc_l};
+  __shared__ int rp_l[GU ? 1 : kTileM];
+  __shared__ float rc_l[GU ? 1 : kTileM];
+  const GLds L{pt_l, rp_l, rc_l, a_l, b_l, rs_l, sc_l};
   const int n_items = *n_tiles * NBK;
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
     const int4 tl = tiles[item / NBK];
