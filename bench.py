@@ -37,7 +37,7 @@ def parse():
                              "qwen3-verify", "hbm-copy"],
                     help="qwen3-prefill: 512 tokens per layer through the grouped "
                          "MFMA path; qwen3-verify: 8 tokens per layer (a speculative "
-                         "verification step) through the small-T grouped decode block, "
+                         "verification step) through the expert block ops.ffn picks, "
                          "against the same tokens decoded one at a time; "
                          "qwen3-stream: 256 decode tokens over a 2048-slot "
                          "pool fed from a pinned host store; hbm-copy: a 1 GiB device "
@@ -57,6 +57,10 @@ def parse():
     ap.add_argument("--engine", default="native", choices=["native", "python"],
                     help="qwen3-stream: the per-layer engine loop in the library "
                          "(moe_engine_layer) or in Python (MoEBlock.streaming_call)")
+    ap.add_argument("--verify-block", default="auto", choices=["auto", "grouped", "decode"],
+                    help="qwen3-verify: the expert block (auto: the one ops.ffn picks for "
+                         "8 tokens, the grouped MFMA block; decode: the small-T decode "
+                         "kernels, bit-identical to one-token calls)")
     ap.add_argument("--profile-tokens", type=int, default=8,
                     help="tokens of the kernel-timing pass after the timed steps")
     return ap.parse_args()
@@ -193,11 +197,13 @@ def prefill(args):
 def verify(args):
     """A speculative verification step (gamma + 1 = 8 draft tokens, the
     multi-token call of spec.py:192-194) on the 48-layer Qwen3 stack: per
-    layer the router for the 8 tokens and the small-T grouped expert block
-    (each distinct expert's weights read once for every token routed to it),
-    the 48 layers captured as one HIP graph.  Interleaved in the same run:
-    the same 8 tokens decoded one at a time by the whole-token kernel.  One
-    step = one verification; value = verified tokens per second."""
+    layer the router for the 8 tokens and the expert block ops.ffn picks
+    for 8 tokens (the grouped MFMA block; `--verify-block decode` runs the
+    small-T decode kernels instead), each distinct expert's weights read once
+    for every token routed to it, the 48 layers captured as one HIP graph.
+    Interleaved in the same run: the same 8 tokens decoded one at a time by
+    the whole-token kernel.  One step = one verification; value = verified
+    tokens per second."""
     import torch
     from moe_stream_amd import geometry as G
     from moe_stream_amd import ops, synth
@@ -206,7 +212,7 @@ def verify(args):
     torch.cuda.set_device(dev)
     T = args.tokens if args.tokens != 64 else 8
     L, slots, geom = 48, 3072, G.QWEN3_30B_A3B
-    stack = PrefillStack(geom, L, slots, T, dev, block="decode", zipf_s=1.1)
+    stack = PrefillStack(geom, L, slots, T, dev, block=args.verify_block, zipf_s=1.1)
     n_steps = args.warmup + args.steps
     xs = synth.hidden_states(T * n_steps, L, geom.d_model, dev, synth.SEED_BASE + 500)
     xs = xs.view(n_steps, T, L, geom.d_model)
@@ -233,8 +239,8 @@ def verify(args):
     ops.check_device_error()
     ver, seq = float(np.median(ver_ms)), float(np.median(seq_ms))
     wbytes = float(np.mean(distinct)) * geom.payload_bytes
-    out = {"metric": "MoE speculative verification tok/s (8 tokens x 48 layers, small-T "
-                     "grouped decode block)",
+    block = stack.block
+    out = {"metric": "MoE speculative verification tok/s (8 tokens x 48 layers)",
            "value": round(T / (ver / 1e3), 1), "unit": "tok/s", "n_gpus": 1,
            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ver, 4),
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -242,8 +248,10 @@ def verify(args):
            "config": {"workload": "qwen3-30b-a3b-moe-stack-verify", "layers": L,
                       "tokens_per_step": T, "top_k": stack.k, "pool_slots": slots,
                       "router_bias": "zipf(1.1) log-popularity",
-                      "launch": "one HIP graph per step: route + 2 grouped decode kernels "
-                                "per layer", "parallelism": "none (1 GPU)"},
+                      "launch": "one HIP graph per step: route + the expert block per layer",
+                      "expert_block": ("grouped bf16 MFMA" if block == "grouped"
+                                       else "small-T decode kernels (pairs grouped by slot)"),
+                      "parallelism": "none (1 GPU)"},
            "ms_per_verify": round(ver, 4),
            "ms_same_tokens_one_at_a_time": round(seq, 4),
            "speedup_vs_one_at_a_time": round(seq / ver, 3),

@@ -70,10 +70,13 @@ def ffn_grouped(pool, slot_refs: torch.Tensor, scores: torch.Tensor,
                 slot_refs, scores, x, out, out_f32, stream, workspace)
 
 
-# Above this many tokens per call the grouped MFMA path runs (each expert's
-# weights then serve several tokens per read); at or below it, the decode
-# kernels (one weight read per routed pair, no grouping pass).
-GROUPED_MIN_TOKENS = 16
+# Above this many tokens per call the grouped MFMA path runs; at or below it,
+# the decode kernels (which group the pairs by slot from 2 tokens on and give
+# results bit-identical to one call per token).  Per step of the 48-layer
+# Qwen3 stack on one MI355X (HIP graph of router + expert block per layer):
+# 4 tokens 2.03 ms (decode kernels) vs 2.02 ms (MFMA block), 8 tokens 2.81
+# vs 2.37 ms, 16 tokens 4.35 vs 2.74 ms.
+GROUPED_MIN_TOKENS = 4
 
 
 def ffn(pool, slot_refs, scores, x, out=None, out_f32=None, stream=None):

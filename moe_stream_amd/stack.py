@@ -266,7 +266,10 @@ class PrefillStack(DecodeStack):
                  device="cuda", block: str = "grouped", **kw):
         """block: "grouped" -- the MFMA block for many tokens (prefill);
         "decode" -- the decode kernels, whose small-T form groups the pairs by
-        slot (a multi-token verification step of a few tokens)."""
+        slot (bit-identical to one call per token); "auto" -- the choice
+        ops.ffn makes for n_tokens."""
+        if block == "auto":
+            block = "grouped" if n_tokens > ops.GROUPED_MIN_TOKENS else "decode"
         super().__init__(geom, n_layers, n_slots, device, **kw)
         import ctypes as C
         self.T = n_tokens

@@ -237,3 +237,37 @@ def test_grouped_out_of_range_ref_reported_not_faulting(qwen_layer):
     assert ei.value.code == _lib.MOE_ERR_DEVICE
     keep = torch.arange(T, device="cuda") != 3
     assert torch.equal(bad[keep], good[keep])
+
+
+@pytest.mark.parametrize("T,block,expect", [(4, "auto", "decode"), (8, "auto", "grouped"),
+                                            (64, "grouped", "grouped")])
+def test_multi_token_stack_graph_replays_equal_eager(T, block, expect):
+    """The multi-token stack (router + expert block per layer, 4 layers)
+    captured once as a HIP graph and replayed for several steps, with eager
+    work of the same stack between the replays: every replay routes and
+    computes exactly what the eager launches do.  `auto` picks the block
+    ops.ffn picks for T tokens."""
+    from moe_stream_amd.stack import PrefillStack
+    st = PrefillStack(G.QWEN3_30B_A3B, 4, 256, T, "cuda", block=block,
+                      seed=20260070 + T, zipf_s=1.1)
+    assert st.block == expect
+    xs = synth.hidden_states(3 * T, st.L, 2048, "cuda", 20260071 + T).view(3, T, st.L, 2048)
+    st.x_in.copy_(xs[0].transpose(0, 1))
+    st.capture()
+    for i in range(3):
+        x_step = xs[i].transpose(0, 1).contiguous()
+        st.run_step(x_step, use_graph=False)
+        torch.cuda.synchronize()
+        ids = torch.stack([b.ids for b in st.bufs]).clone()
+        y_ref = st.y.clone()
+        st.run_step(x_step, use_graph=True)
+        torch.cuda.synchronize()
+        ops.check_device_error()
+        assert torch.equal(torch.stack([b.ids for b in st.bufs]), ids), i
+        assert torch.equal(st.y, y_ref), i
+    Lx = 1                       # ops.ffn runs the same block at this T
+    y = ops.ffn(st.pool, st.bufs[Lx].slot_refs, st.bufs[Lx].scores, st.x_in[Lx])
+    torch.cuda.synchronize()
+    assert torch.equal(y, st.y[Lx])
+    del st
+    torch.cuda.empty_cache()
