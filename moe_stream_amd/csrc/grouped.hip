@@ -498,7 +498,8 @@ __device__ __forceinline__ void grouped_item(
         }
     }
   };
-  // one group of the quad in LDS (gi: its index in the quad, a constant)
+  // One group of the quad in LDS (gi: its index in the quad, a constant), in
+  // source order: decode, MFMAs, fold (down, held to 128 VGPRs)
   auto group = [&](int g, int gi) {
     if (QS && gi == 0) {   // the quad's scales, 4 halfwords per lane and row
 #pragma unroll
@@ -544,18 +545,107 @@ __device__ __forceinline__ void grouped_item(
           // c0 (the second MFMA's accumulator input) stays allocated until the
           // fold has read c: this compiler otherwise reuses its registers a
           // few instructions after the MFMA issues, before the MFMA has read
-          // them
-          asm volatile("" ::"v"(c0), "v"(acc[rb][cb][j]));
+          // them.  The empty asm passes acc through (a data dependency, not a
+          // side effect), so it orders no memory access and LDS reads of
+          // later row blocks can still be issued ahead of this fold
+          asm("" : "+v"(acc[rb][cb][j]) : "v"(c0));
         }
     }
+  };
+  // One group of the quad in LDS (gi: its index in the quad, a constant), in
+  // three steps so the quad can run them as a software pipeline: its B
+  // fragments decoded (and its scales), its MFMAs into fresh 16x16 blocks, and
+  // the fold of those blocks into the output by S.  The quad issues group
+  // gi's MFMAs, then decodes group gi + 1 and folds group gi, so that VALU
+  // work independent of the MFMAs in flight follows them.
+  struct GFrag {
+    uint4 b0[NPROJ][CPW], b1[NPROJ][CPW];
+    float S[NPROJ][CPW];
+  };
+  struct GOut {
+    f32x4_t c0[NMB][CPW][NPROJ], c[NMB][CPW][NPROJ];
+  };
+  auto decode = [&](int g, int gi, GFrag &f) {
+    if (QS && gi == 0) {   // the quad's scales, 4 halfwords per lane and row
+#pragma unroll
+      for (int j = 0; j < NPROJ; ++j)
+#pragma unroll
+        for (int cb = 0; cb < CPW; ++cb) {
+          const int nl = (wave * CPW + cb) * 16 + col;
+          s4[j][cb] = scq[((2 * j) * NQ + (g >> 2)) * NB + nl];
+        }
+    }
+    const char *bq = reinterpret_cast<const char *>(L.b);
+    const uint32_t cpos = (uint32_t)(gi * 32 + kq * 8);   // logical chunk and half
+#pragma unroll
+    for (int j = 0; j < NPROJ; ++j)
+#pragma unroll
+      for (int cb = 0; cb < CPW; ++cb) {
+        const uint2 cw = *reinterpret_cast<const uint2 *>(bq + bfr[j][cb] + (cpos ^ bx[j][cb]));
+        f.b0[j][cb] = b_frag(cw.x);
+        f.b1[j][cb] = b_frag(cw.y);
+        if (QS) {
+          const uint32_t h = gi < 2 ? s4[j][cb].x : s4[j][cb].y;
+          f.S[j][cb] = __uint_as_float((gi & 1) ? (h & 0xffff0000u) : (h << 16));
+        } else {
+          const int nl = (wave * CPW + cb) * 16 + col;
+          f.S[j][cb] = bf16_to_f32(sch[(2 * j) * SCH + nl * NG + g]);
+        }
+      }
+  };
+  auto mma = [&](int gi, const GFrag &f, GOut &o) {
+    const uint4 *al = L.a[gi];
+#pragma unroll
+    for (int rb = 0; rb < NMB; ++rb) {
+      const int r = rb * 16 + col;
+      const uint4 a0 = al[r * 8 + ((2 * kq) ^ (r & 7))], a1 = al[r * 8 + ((2 * kq + 1) ^ (r & 7))];
+#pragma unroll
+      for (int cb = 0; cb < CPW; ++cb)
+#pragma unroll
+        for (int j = 0; j < NPROJ; ++j) {
+          o.c0[rb][cb][j] = mfma16x16x32(a0, f.b0[j][cb], (f32x4_t){0.f, 0.f, 0.f, 0.f});
+          o.c[rb][cb][j] = mfma16x16x32(a1, f.b1[j][cb], o.c0[rb][cb][j]);
+        }
+    }
+  };
+  auto fold = [&](const GFrag &f, const GOut &o) {
+#pragma unroll
+    for (int rb = 0; rb < NMB; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < CPW; ++cb)
+#pragma unroll
+        for (int j = 0; j < NPROJ; ++j) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[rb][cb][j][e] += f.S[j][cb] * o.c[rb][cb][j][e];
+          // c0 (the second MFMA's accumulator input) stays allocated until the
+          // fold has read c: this compiler otherwise reuses its registers a
+          // few instructions after the MFMA issues, before the MFMA has read
+          // them.  The empty asm passes acc through (a data dependency, not a
+          // side effect), so it orders no memory access
+          asm("" : "+v"(acc[rb][cb][j]) : "v"(o.c0[rb][cb][j]));
+        }
   };
   // one quad: its groups from LDS, its bias term; then (all waves done with
   // the quad) the next quad's operands from registers to LDS and the loads of
   // the one after
   auto quad = [&](int q, int ng, bool next, int ng_next, bool refill, int ng_refill) {
+    if (GU && QS) {   // gate/up: the pipelined order (down keeps 4 waves per
+                      // SIMD; with NG % 4 != 0 it would not fit 256 VGPRs)
+      GFrag fr[2];
+      GOut o;
+      decode(4 * q, 0, fr[0]);
 #pragma unroll
-    for (int gi = 0; gi < 4; ++gi)
-      if (gi < ng) group(4 * q + gi, gi);
+      for (int gi = 0; gi < 4; ++gi) {
+        if (gi >= ng) continue;
+        mma(gi, fr[gi & 1], o);
+        if (gi + 1 < ng) decode(4 * q + gi + 1, gi + 1, fr[(gi + 1) & 1]);
+        fold(fr[gi & 1], o);
+      }
+    } else {
+#pragma unroll
+      for (int gi = 0; gi < 4; ++gi)
+        if (gi < ng) group(4 * q + gi, gi);
+    }
     bias_step(q, s4);
     if (next) {
       __syncthreads();
