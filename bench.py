@@ -590,7 +590,7 @@ def main():
         ms = np.array([a.elapsed_time(b) for a, b in launch_ev])
         avg_ms, med_ms, n = float(ms.mean()), float(np.median(ms)), len(ms)
         per_launch = stack.expert_bytes_per_token() + router_bytes
-        kname = "stack_decode_kernel"
+        kname = "stack_decode_kernel" if stack.geom.d_model == 2048 else "stack_wide_kernel"
     else:
         per_launch = stack.k * sum(c.nbytes for c in stack.geom.components
                                    if c.name.startswith(("gate_proj", "up_proj")))
