@@ -57,6 +57,10 @@ def parse():
     ap.add_argument("--engine", default="native", choices=["native", "python"],
                     help="qwen3-stream: the per-layer engine loop in the library "
                          "(moe_engine_layer) or in Python (MoEBlock.streaming_call)")
+    ap.add_argument("--pool-layout", default="records", choices=["records", "components"],
+                    help="qwen3-stream: slots holding whole records (fills by the copy "
+                         "engines, one copy per record) or component arrays (fills by "
+                         "copy kernels)")
     ap.add_argument("--verify-block", default="auto", choices=["auto", "grouped", "decode"],
                     help="qwen3-verify: the expert block (auto: the one ops.ffn picks for "
                          "8 tokens, the grouped MFMA block; decode: the small-T decode "
@@ -314,7 +318,8 @@ def stream(args):
     n_tok = args.tokens if args.tokens != 64 else 256
     t_build = time.perf_counter()
     native = args.engine == "native"
-    st = StreamingStack(geom, L, slots, dev, zipf_s=1.1, native=native)
+    st = StreamingStack(geom, L, slots, dev, zipf_s=1.1, native=native,
+                        pool_layout=args.pool_layout)
     t_build = time.perf_counter() - t_build
 
     def bytes_read():
@@ -358,6 +363,9 @@ def stream(args):
                       "pool_slots": slots, "store_records": L * geom.n_experts,
                       "record_bytes": geom.record_bytes, "tokens": n_tok,
                       "evict": st.pool.evict, "prefetch": "lookahead depth 1, widen 1",
+                      "pool_layout": args.pool_layout,
+                      "fills": ("hipMemcpyAsync per record (copy engines)"
+                                if args.pool_layout == "records" else "copy kernels"),
                       "engine": ("moe_engine_layer (library)" if native
                                  else "MoEBlock.streaming_call (Python)"),
                       "router_bias": "zipf(1.1) log-popularity",

@@ -272,10 +272,14 @@ int moe_slot_lookup(const int32_t *table, int32_t E, const int32_t *ids,
  * memory laid out like pool->store, src_n_records records of
  * src_record_bytes; NULL means pool->store with the view's record size and
  * count), dst_slots: pool slots.  Host index arrays; every index is range
- * checked on the host (MOE_ERR_INVALID) before anything is enqueued.  Enqueued on `stream`: a source the GPU can
- * read (HBM or pinned host memory) is copied by kernels, up to 160 records
- * per launch; pageable memory by hipMemcpyAsync per component.  Replaces
- * ExpertPool._read (engine_v3.py:255-290). */
+ * checked on the host (MOE_ERR_INVALID) before anything is enqueued.  Enqueued on `stream`.
+ * A pool in the record layout (every component c at base + comp_offset[c]
+ * of one base with slot stride src_record_bytes, i.e. each slot holds one
+ * whole record) takes one hipMemcpyAsync per record (the copy engines, no
+ * compute units).  Otherwise a source the GPU can read (HBM or pinned host
+ * memory) is copied by kernels, up to 160 records per launch, and pageable
+ * memory by hipMemcpyAsync per component.  Replaces ExpertPool._read
+ * (engine_v3.py:255-290). */
 int moe_fill_slots(const moe_pool_view *pool, const void *src_store,
                    int64_t src_record_bytes, int64_t src_n_records,
                    const int64_t *src_records, const int32_t *dst_slots, int32_t n,

@@ -616,6 +616,17 @@ const char *kernel_address(const void *p, bool *host) {
   return nullptr;
 }
 
+// The record layout: component c at base + comp_offset[c] with slot stride
+// `rb` for every c, so slot s holds one whole record at base + s * rb.
+bool record_layout(const moe_pool_view *pool, int64_t rb) {
+  const char *b0 = static_cast<const char *>(pool->base[0]) - pool->comp_offset[0];
+  for (int c = 0; c < pool->n_components; ++c)
+    if (pool->slot_bytes[c] != rb ||
+        static_cast<const char *>(pool->base[c]) - pool->comp_offset[c] != b0)
+      return false;
+  return pool->n_slots > 0;
+}
+
 }  // namespace
 
 int moe_fill_slots(const moe_pool_view *pool, const void *src_store,
@@ -642,6 +653,17 @@ int moe_fill_slots(const moe_pool_view *pool, const void *src_store,
     if (rec < 0 || rec >= nrec)
       return fail(MOE_ERR_INVALID, "record %lld outside [0, %lld)", (long long)rec,
                   (long long)nrec);
+  }
+  // A pool in the record layout (every component at its record offset from
+  // one base, slot stride = the source's record size) holds each slot's
+  // record contiguously: one hipMemcpyAsync per record, which the copy
+  // engines carry out without occupying compute units.
+  if (record_layout(pool, rb)) {
+    char *base = static_cast<char *>(pool->base[0]) - pool->comp_offset[0];
+    for (int32_t i = 0; i < n; ++i)
+      MOE_HIP(hipMemcpyAsync(base + (int64_t)dst_slots[i] * rb, src + src_records[i] * rb,
+                             (size_t)rb, hipMemcpyDefault, s));
+    return MOE_OK;
   }
   // Copy kernels for a source the GPU can read (HBM, or pinned host memory
   // over the link: one launch per batch instead of a copy call per

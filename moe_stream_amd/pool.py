@@ -4,10 +4,18 @@ Storage follows engine_v3.py:180-206: one device array per component,
 shaped [n_slots, *shape] in its final dtype (uint32 codes are held in int32
 tensors, bit-identical), named "{proj}.{part}", exposed as `.views`.
 
+Two layouts of that storage in HBM.  "components": the component arrays
+back to back in one allocation (the layout the whole-token decode kernels
+require).  "records": slot s holds one whole store record at s x
+record_bytes, each component view a strided view into it (the same
+[n_slots, *shape] arrays to every reader); ExpertPool's default, since a fill
+is then one copy per record.
+
 Fills replace ExpertPool._read (engine_v3.py:255-290): a record of the
 expert store (pinned host memory or HBM, repacked layout) is copied into
-the slot's component rows by hipMemcpyAsync, on a side stream for
-prefetches and on the compute stream for demand misses.  Completion is an
+the slot -- one hipMemcpyAsync per record on the copy engines for the
+record layout, copy kernels otherwise -- on a side stream for prefetches
+and on the compute stream for demand misses.  Completion is an
 event: an acquire of a key whose prefetch is still in flight makes the
 compute stream wait on that event instead of blocking the host, and a
 prefetch fill first waits for the compute work already enqueued, so a slot
@@ -75,18 +83,36 @@ def _torch_dtype(c) -> torch.dtype:
 class SlotPool:
     """Device arrays of the pool and the C view the kernels read."""
 
-    def __init__(self, geom: Geometry, n_slots: int, device="cuda", store=None):
+    def __init__(self, geom: Geometry, n_slots: int, device="cuda", store=None,
+                 layout: str = "components"):
+        if layout not in ("components", "records"):
+            raise ValueError(f"layout {layout!r}: 'components' or 'records'")
         self.geom = geom
         self.n_slots = n_slots
         self.device = _norm_device(device)
-        # one array per component, [n_slots, *shape] in its final dtype, all
-        # in one allocation back to back in component order
-        self._buf = torch.zeros(n_slots * geom.payload_bytes, dtype=torch.uint8,
-                                device=self.device)
+        self.layout = layout
         self.views = {}
-        for c in geom.components:
-            part = self._buf[n_slots * c.offset:n_slots * (c.offset + c.nbytes)]
-            self.views[c.name] = part.view(_torch_dtype(c)).view(n_slots, *c.shape)
+        if layout == "components":
+            # one array per component, [n_slots, *shape] in its final dtype,
+            # all in one allocation back to back in component order
+            self._buf = torch.zeros(n_slots * geom.payload_bytes, dtype=torch.uint8,
+                                    device=self.device)
+            for c in geom.components:
+                part = self._buf[n_slots * c.offset:n_slots * (c.offset + c.nbytes)]
+                self.views[c.name] = part.view(_torch_dtype(c)).view(n_slots, *c.shape)
+        else:
+            # slot s = store record layout at s * record_bytes; component c at
+            # its record offset (16-byte multiples, so every dtype view aligns)
+            rb = geom.record_bytes
+            self._buf = torch.zeros(n_slots * rb, dtype=torch.uint8, device=self.device)
+            for c in geom.components:
+                dt = _torch_dtype(c)
+                es = torch.empty((), dtype=dt).element_size()
+                assert rb % es == 0 and c.offset % es == 0
+                inner = [int(np.prod(c.shape[i + 1:])) for i in range(len(c.shape))]
+                self.views[c.name] = torch.as_strided(
+                    self._buf.view(dt), (n_slots, *c.shape), (rb // es, *inner),
+                    c.offset // es)
         self.pool_bytes = sum(a.numel() * a.element_size() for a in self.views.values())
         self.store = store           # torch uint8 [n_records, record_bytes] or HostStore
         self._view = None
@@ -97,9 +123,10 @@ class SlotPool:
             v = _lib.PoolView()
             v.n_components = self.geom.n_components
             v.n_slots = self.n_slots
+            rec = self.layout == "records"
             for i, c in enumerate(self.geom.components):
                 v.base[i] = self.views[c.name].data_ptr()
-                v.slot_bytes[i] = c.nbytes
+                v.slot_bytes[i] = self.geom.record_bytes if rec else c.nbytes
                 v.comp_offset[i] = c.offset
             s = self.store
             if isinstance(s, torch.Tensor):
@@ -158,7 +185,7 @@ class ExpertPool(SlotPool):
     def __init__(self, model_dir, n_slots: int = N_SLOTS, n_workers: int = N_WORKERS,
                  store=None, device="cuda", evict: str | None = None, depths=(1,),
                  widen: int = 1, side_stream: torch.cuda.Stream | None = None,
-                 n_layers: int | None = None):
+                 n_layers: int | None = None, layout: str = "records"):
         if isinstance(model_dir, Geometry):
             geom = model_dir
             if store is None:
@@ -170,7 +197,7 @@ class ExpertPool(SlotPool):
             if store is None:
                 store = sf.to_host_store(n_workers=n_workers)
             n_layers = n_layers or sf.index.n_layers
-        super().__init__(geom, n_slots, device, store)
+        super().__init__(geom, n_slots, device, store, layout=layout)
         self.n_workers = n_workers
         self.n_experts = geom.n_experts
         self.n_layers = n_layers or geom.n_layers

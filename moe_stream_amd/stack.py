@@ -326,17 +326,21 @@ class StreamingStack:
     layer, streaming_call (route + lookahead, one host synchronisation,
     prefetch of the predicted layer-L+1 experts, acquire, the expert block;
     engine_v3.py:493-609) on an ExpertPool whose fills come from a pinned
-    host store by hipMemcpyAsync, prefetches on a side stream.  Store
+    host store by hipMemcpyAsync (one per record), prefetches on a side
+    stream.  Store
     records, routers and inputs are those of DecodeStack with the same seed,
     so the two produce identical outputs."""
 
     def __init__(self, geom: Geometry, n_layers: int, n_slots: int, device="cuda",
                  seed: int = synth.SEED_BASE + 2, zipf_s: float | None = 1.1,
                  router_bias: bool = False, widen: int = 1, host_store=None,
-                 evict: str | None = None, native: bool = False):
+                 evict: str | None = None, native: bool = False,
+                 pool_layout: str = "records"):
         """native: run each layer's engine loop in the library
         (moe_engine_layer) instead of MoEBlock.streaming_call; same policy,
-        fills and kernels, no Python frame between a layer's steps."""
+        fills and kernels, no Python frame between a layer's steps.
+        pool_layout: "records" (a fill is one copy-engine copy per record) or
+        "components" (copy-kernel fills)."""
         from .block import MoEBlock
         from .pool import ExpertPool
         self.geom = geom
@@ -347,7 +351,7 @@ class StreamingStack:
         self.store = host_store if host_store is not None else \
             synth.make_host_store(geom, n_layers * self.E, self.device, seed)
         self.pool = ExpertPool(geom, n_slots, store=self.store, device=self.device, evict=evict,
-                               widen=widen, n_layers=n_layers)
+                               widen=widen, n_layers=n_layers, layout=pool_layout)
         self.W, self.bias, self.logpop = routers(geom, n_layers, self.device, seed,
                                                  zipf_s, router_bias)
         self.blocks = []

@@ -1,8 +1,9 @@
 """Slot fills (the role of ExpertPool._read, engine_v3.py:255-290): every
 component of every filled slot holds exactly its record's bytes at the
 record's component offset (verify_pool.py:64-87), for device-resident
-sources (copy kernels, batches wider than one launch) and for a pinned host
-store (DMA copies)."""
+sources and for a pinned host store, into a pool of component arrays (copy
+kernels, batches wider than one launch) and into a pool of whole records
+(one copy-engine copy per record)."""
 import numpy as np
 import pytest
 import torch
@@ -23,14 +24,15 @@ def _check(pool, store_u8, recs, slots):
         assert torch.equal(got, want), c.name
 
 
+@pytest.mark.parametrize("layout", ["components", "records"])
 @pytest.mark.parametrize("geom,n_records,n_slots,n_fill", [
     (G.QWEN3_30B_A3B, 400, 512, 347),      # three launches of the batched kernel
     (G.GPT_OSS_120B, 24, 40, 21),          # 12 components, 5760-byte biases
     (G.SMALL, 64, 64, 64),
 ])
-def test_device_source_fills_are_exact(geom, n_records, n_slots, n_fill):
+def test_device_source_fills_are_exact(geom, n_records, n_slots, n_fill, layout):
     store = synth.make_store(geom, n_records, "cuda", 20260701)
-    pool = SlotPool(geom, n_slots, "cuda", store=store)
+    pool = SlotPool(geom, n_slots, "cuda", store=store, layout=layout)
     rng = np.random.default_rng(20260702)
     recs = rng.choice(n_records, n_fill, replace=False)
     slots = rng.permutation(n_slots)[:n_fill]
@@ -45,11 +47,12 @@ def test_device_source_fills_are_exact(geom, n_records, n_slots, n_fill):
     _check(pool, store, recs[n_fill // 2:], slots[n_fill // 2:])
 
 
-def test_pinned_host_source_fills_are_exact():
+@pytest.mark.parametrize("layout", ["components", "records"])
+def test_pinned_host_source_fills_are_exact(layout):
     geom = G.QWEN3_30B_A3B
     host = synth.make_host_store(geom, 40, "cuda", 20260703)
     dev = synth.make_store(geom, 40, "cuda", 20260703)
-    pool = SlotPool(geom, 48, "cuda", store=host)
+    pool = SlotPool(geom, 48, "cuda", store=host, layout=layout)
     recs, slots = np.arange(40)[::-1].copy(), np.arange(3, 43)
     pool.fill(recs, slots)
     torch.cuda.synchronize()

@@ -51,11 +51,15 @@ def test_streaming_equals_resident_stack(stacks):
     assert 0.0 <= st.recall() <= 1.0
 
 
-def test_native_engine_equals_resident_stack(stacks):
+@pytest.mark.parametrize("layout", ["records", "components"])
+def test_native_engine_equals_resident_stack(stacks, layout):
     """The engine loop in the library (moe_engine_layer): same outputs as the
-    HBM-resident stack, the policy's statistics and byte counts consistent."""
+    HBM-resident stack, the policy's statistics and byte counts consistent,
+    with fills by the copy engines (slots holding whole records) or by copy
+    kernels (component arrays)."""
     geom, dec, _, xs = stacks
-    st = StreamingStack(geom, L, 40, "cuda", seed=20260601, zipf_s=1.1, native=True)
+    st = StreamingStack(geom, L, 40, "cuda", seed=20260601, zipf_s=1.1, native=True,
+                        pool_layout=layout)
     for t in range(xs.shape[0]):
         dec.run_token(xs[t], use_graph=False)
         y = st.token(xs[t])

@@ -32,3 +32,37 @@ def test_stats_keys_are_the_reference_keys():
     src = inspect.getsource(ExpertPool.stats)
     for k in REFERENCE_STATS_KEYS:
         assert f"{k}=" in src, k
+
+
+def test_record_layout_views_address_whole_records():
+    """The record layout on host memory: slot s holds a store record at
+    s * record_bytes, every component view reads its bytes at the record's
+    component offset, and the C view carries one base with slot stride =
+    record size (the form moe_fill_slots copies with one call per record)."""
+    import numpy as np
+    import torch
+    from moe_stream_amd import geometry as G
+    from moe_stream_amd.pool import SlotPool
+    for geom in (G.SMALL, G.GPT_OSS_120B):
+        n = 3
+        pool = SlotPool(geom, n, "cpu", layout="records")
+        rb = geom.record_bytes
+        rng = np.random.default_rng(5)
+        recs = rng.integers(0, 256, (n, rb), dtype=np.uint8)
+        pool._buf.copy_(torch.from_numpy(recs.reshape(-1)))
+        v = pool.c_view()
+        base = pool._buf.data_ptr()
+        for i, c in enumerate(geom.components):
+            got = pool.views[c.name]
+            assert tuple(got.shape) == (n, *c.shape)
+            for s in range(n):
+                b = got[s].contiguous().view(torch.uint8).numpy().reshape(-1)
+                np.testing.assert_array_equal(b, recs[s, c.offset:c.offset + c.nbytes])
+            assert v.base[i] == base + c.offset and v.slot_bytes[i] == rb
+            assert v.comp_offset[i] == c.offset
+    try:
+        SlotPool(G.SMALL, 2, "cpu", layout="rows")
+    except ValueError:
+        pass
+    else:
+        raise AssertionError("unknown layout accepted")
