@@ -132,6 +132,18 @@ def test_grouped_qwen3_matches_oracle(qwen_layer):
     _grouped_vs_oracle(qwen_layer, x, "qwen3 grouped T=48")
 
 
+@pytest.mark.parametrize("T", [5, 12])
+def test_grouped_few_tokens_matches_oracle(qwen_layer, T):
+    """A few tokens per call (a verification step): ops.ffn takes the grouped
+    MFMA block above 4 tokens, whose tiles then hold one to a few rows."""
+    assert T > ops.GROUPED_MIN_TOKENS
+    x = bf16_randn((T, 2048), seed=20260060 + T)
+    bufs, out, out32 = _grouped_vs_oracle(qwen_layer, x, f"qwen3 grouped T={T}")
+    y = ops.ffn(qwen_layer.pool, bufs.slot_refs, bufs.scores, x)
+    torch.cuda.synchronize()
+    assert torch.equal(y, out)
+
+
 def test_grouped_gptoss_matches_oracle():
     layer = Layer(G.GPT_OSS_120B, 136, seed=20260047, router_bias=True)
     x = bf16_randn((40, 2880), seed=20260048)
