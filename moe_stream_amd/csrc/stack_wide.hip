@@ -113,18 +113,27 @@ __device__ __forceinline__ void get_acts_wide(int tid, const uint64_t *hf, uint3
                                               const Abort &ab, uint4 (&p)[HPL]) {
   const int lane = tid & 63;
   uint32_t spins = 0;
+  // a piece whose 4 entries all carried the flag is kept and not read again:
+  // later rounds read only what was missing (every workgroup re-reading all
+  // of its pieces per round loads the path the polls share)
+  static_assert(HPL <= 32, "one bit per piece");
+  uint32_t got = 0;   // bit i: piece i complete
   while (true) {
     bool ok = true;
 #pragma unroll
     for (int i = 0; i < HPL; ++i) {
+      if ((got >> i) & 1u) continue;
       const uint64_t *e = hf + 4 * min(lane + 64 * i, HU4 - 1);
       uint64_t v[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         v[q] = __hip_atomic_load(e + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      bool ok_i = true;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) ok = ok && (uint32_t)(v[q] >> 32) == fl;
+      for (int q = 0; q < 4; ++q) ok_i = ok_i && (uint32_t)(v[q] >> 32) == fl;
       p[i] = make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+      got |= (uint32_t)ok_i << i;
+      ok = ok && ok_i;
     }
     if (__ballot(!ok) == 0) break;
     if (ab.gave_up(++spins)) break;
@@ -531,6 +540,29 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
         lds_wait_count(&fsync, C::WAVES_U * ++nfs);
       }
       if (wave == 0) trace_mark(a, l, TR_FIXED);
+      // ---- gate/up wave p polls position p's activations and stages them
+      // for the down wave of that position: it has no loads in flight here,
+      // while the down waves' polls would return only after their
+      // direct-to-LDS down-row loads (loads complete in order)
+      if (uact) {
+        const int p = wave;
+        const bool fix = pos_fix[p] >= 0;
+        uint4 pv[HPL];
+        get_acts_wide<HU4, HPL>(tid, (fix ? hfix : hpred) + (size_t)p * (F / 2), fl, ab, pv);
+        if (dact) {
+#pragma unroll
+          for (int it = 0; it < HPL; ++it) {
+            const int i = lane + 64 * it;
+            float sm = 0.f;
+            if (i < HU4) sm = stage_piece<UF>(hact_l[p], i, pv[it]);
+            sm += dpp_f<kDppQuadXor1>(sm);
+            sm += dpp_f<kDppQuadXor2>(sm);
+            if (i < HU4 && (i & 3) == 0) hsum_l[p][i >> 2] = sm;
+          }
+        }
+        lds_set_flag(&hready[p], fl);
+        if (wave == 2) trace_mark(a, l, TR_D_WAITED);
+      }
       lds_arrive(&dsync);
       // ---- gate/up loads of layer l+1's prediction, once this workgroup's
       // activation polls are done (loads queued ahead of them would delay
@@ -751,26 +783,9 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
           dbias_l[p][lane] = dbias ? bf16_to_f32(dbias[drow0 + lane]) : 0.f;
         }
       }
-      if (uact) {
-        const bool fix = pos_fix[p] >= 0;
-        uint4 pv[HPL];
-        get_acts_wide<HU4, HPL>(tid, (fix ? hfix : hpred) + (size_t)p * (F / 2), fl, ab, pv);
-        if (dact) {
-#pragma unroll
-          for (int it = 0; it < HPL; ++it) {
-            const int i = lane + 64 * it;
-            float sm = 0.f;
-            if (i < HU4) sm = stage_piece<UF>(hact_l[p], i, pv[it]);
-            sm += dpp_f<kDppQuadXor1>(sm);
-            sm += dpp_f<kDppQuadXor2>(sm);
-            if (i < HU4 && (i & 3) == 0) hsum_l[p][i >> 2] = sm;
-          }
-        }
-        lds_set_flag(&hready[p], fl);
-        if (wave == W_ROUTER) trace_mark(a, l, TR_D_WAITED);
-      }
       if (dact) {
         __builtin_amdgcn_s_waitcnt(0);   // this wave's direct-to-LDS loads landed
+        lds_wait_flag(&hready[p], fl);   // the activations, staged by gate/up wave p
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         wide_down_rows<C>(lane, a, dref, sel_sc[r], dcode_l[p],
                           reinterpret_cast<const uint16_t *>(&dsc_l[p][0][0]), hact_l[p], hsum_l[p],
