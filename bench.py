@@ -61,6 +61,9 @@ def parse():
                     help="qwen3-stream: slots holding whole records (fills by the copy "
                          "engines, one copy per record) or component arrays (fills by "
                          "copy kernels)")
+    ap.add_argument("--depths", default="1",
+                    help="qwen3-stream: the prefetch depths, comma-separated (the "
+                         "reference's PF_DEPTH list), e.g. 1,2")
     ap.add_argument("--verify-block", default="auto", choices=["auto", "grouped", "decode"],
                     help="qwen3-verify: the expert block (auto: the one ops.ffn picks for "
                          "8 tokens, the grouped MFMA block; decode: the small-T decode "
@@ -318,8 +321,9 @@ def stream(args):
     n_tok = args.tokens if args.tokens != 64 else 256
     t_build = time.perf_counter()
     native = args.engine == "native"
+    depths = tuple(int(d) for d in args.depths.split(","))
     st = StreamingStack(geom, L, slots, dev, zipf_s=1.1, native=native,
-                        pool_layout=args.pool_layout)
+                        pool_layout=args.pool_layout, depths=depths)
     t_build = time.perf_counter() - t_build
 
     def bytes_read():
@@ -362,7 +366,7 @@ def stream(args):
            "config": {"workload": "qwen3-30b-a3b-moe-stack-streaming", "layers": L,
                       "pool_slots": slots, "store_records": L * geom.n_experts,
                       "record_bytes": geom.record_bytes, "tokens": n_tok,
-                      "evict": st.pool.evict, "prefetch": "lookahead depth 1, widen 1",
+                      "evict": st.pool.evict, "prefetch": f"lookahead depths {','.join(map(str, depths))}, widen 1",
                       "pool_layout": args.pool_layout,
                       "fills": ("hipMemcpyAsync per record (copy engines)"
                                 if args.pool_layout == "records" else "copy kernels"),

@@ -370,6 +370,18 @@ int moe_engine_destroy(moe_engine *e);
 int moe_engine_layer(moe_engine *e, int32_t layer, const uint16_t *x, const uint16_t *W,
                      const uint16_t *bias, int32_t mode, int32_t renorm,
                      const uint16_t *W_next, const uint16_t *bias_next, uint16_t *y);
+/* One layer with a list of prefetch depths (the reference's PF_DEPTH list,
+ * engine_v3.py:61, 509-527): for each depths[j] > 0 whose target layer
+ * (layer + depths[j]) is in the stack and whose router W_look[j] is not NULL,
+ * the top-k_pred experts of that router on x are prefetched for the target
+ * layer, in the list's order; recall is counted for depths[0] only.
+ * bias_look may be NULL (no router biases) or hold NULL entries.
+ * n_depths <= 4.  moe_engine_layer is this call with depths = {1}. */
+int moe_engine_layer_depths(moe_engine *e, int32_t layer, const uint16_t *x,
+                            const uint16_t *W, const uint16_t *bias, int32_t mode,
+                            int32_t renorm, const int32_t *depths, int32_t n_depths,
+                            const uint16_t *const *W_look, const uint16_t *const *bias_look,
+                            uint16_t *y);
 /* out[5] = bytes read into the pool, bytes read on the critical path
  * (misses), routed experts that were predicted, routed experts counted for
  * recall, prefetches still pending */

@@ -47,7 +47,8 @@ EXPORTS = (
     "moe_policy_create", "moe_policy_destroy", "moe_policy_prefetch",
     "moe_policy_acquire", "moe_policy_complete", "moe_policy_lookup",
     "moe_policy_is_pending", "moe_policy_table", "moe_policy_stats",
-    "moe_engine_create", "moe_engine_destroy", "moe_engine_layer", "moe_engine_counters",
+    "moe_engine_create", "moe_engine_destroy", "moe_engine_layer", "moe_engine_layer_depths",
+    "moe_engine_counters",
 )
 
 MOE_EVICT_LFU = 0
@@ -131,6 +132,7 @@ def _declare(lib):
                                         I32, P, P, I64, I64, P, P, C.POINTER(C.c_void_p)]),
         "moe_engine_destroy": (C.c_int, [P]),
         "moe_engine_layer": (C.c_int, [P, I32, P, P, P, I32, I32, P, P, P]),
+        "moe_engine_layer_depths": (C.c_int, [P, I32, P, P, P, I32, I32, P, I32, P, P, P]),
         "moe_engine_counters": (C.c_int, [P, P]),
     }
     for name, (res, args) in sig.items():

@@ -14,6 +14,14 @@
 //      compute stream, in-flight prefetches become stream waits;
 //   6. the expert block (the decode kernels) on the compute stream, its slot
 //      refs carried in the kernel arguments (no copy to the device).
+// Further prefetch depths (the reference's PF_DEPTH list, engine_v3.py:61,
+// 509-527; moe_engine_layer_depths): the first depth's router rides in the
+// route launch of step 1; the router of each further depth d runs on x_l as
+// a route launch of its own on the engine's lookahead stream beside step 1,
+// and the host waits for all of them at once.  Their predictions are
+// prefetched after the first depth's, in the list's order (the policy sees
+// the reference's call sequence), and their copies are issued once the
+// expert block is enqueued, since none is needed before layer l+2.
 // Reuse of the pinned buffers is safe by stream order: the host rewrites
 // them only after it has seen the next layer's router output, and that
 // router started after the previous expert block completed.
@@ -29,10 +37,7 @@
 namespace {
 
 constexpr int kEngineMaxPred = 64;
-
-struct PendingFill {
-  hipEvent_t ev;
-};
+constexpr int kEngineMaxDepths = 4;  // first depth + 3 further ones
 
 }  // namespace
 
@@ -54,12 +59,23 @@ struct moe_engine {
   // addresses of ids and predictions
   int32_t *h_ids = nullptr, *h_pred = nullptr;
   int32_t *k_ids = nullptr, *k_pred = nullptr;
+  // further lookahead depths: their predictions (pinned, as above), the
+  // lookahead stream their route launches run on, the event that orders
+  // them after x, and the launches' own ids, scores and workspace
+  int32_t *h_predx[kEngineMaxDepths - 1] = {}, *k_predx[kEngineMaxDepths - 1] = {};
+  hipStream_t look = nullptr;
+  hipEvent_t x_ready = nullptr;
+  int32_t *d_idsx = nullptr;
+  float *d_scoresx = nullptr;
+  void *d_route_wsx = nullptr;
   int32_t h_refs[MOE_MAX_TOPK] = {};               // this layer's slot refs
   // bookkeeping
   std::unordered_map<int64_t, hipEvent_t> pending;   // key -> its fill's event
   std::vector<hipEvent_t> free_events;
-  std::vector<int32_t> last_pred;                    // unique prediction for layer l+1
-  int32_t last_pred_layer = -1;
+  // the first depth's unique prediction per target layer, taken when that
+  // layer routes (the reference's _PRED dict, engine_v3.py:521-523)
+  std::vector<std::vector<int32_t>> pred_for;
+  std::vector<char> pred_set;
   int64_t bytes_read = 0, bytes_exposed = 0, recall_hit = 0, recall_total = 0;
 };
 
@@ -105,19 +121,23 @@ int engine_poll(moe_engine *e) {
   return MOE_OK;
 }
 
-// Wait for the router's ids (and predictions) in pinned memory.  Every entry
-// is -1 before the launch and is written once with an id in [0, E), so all
-// entries non-negative means the output is complete.  The stream is queried
-// only once a wait has run past 1 ms (and every 1 ms after), so that a failed
-// launch ends the wait with its error: a query on every pass of a normal
-// (~30 us) wait cost the loop 13 % of its rate.
-int engine_wait_route(moe_engine *e, bool look) {
+// Wait for the router's ids and the predictions of n_pred lookahead
+// launches in pinned memory.  Every entry is -1 before the launches and is
+// written once with an id in [0, E), so all entries non-negative means the
+// outputs are complete.  The streams are queried only once a wait has run
+// past 1 ms (and every 1 ms after), so that a failed launch ends the wait with
+// its error: a query on every pass of a normal (~30 us) wait cost the loop
+// 13 % of its rate.
+int engine_wait_route(moe_engine *e, const int32_t *const *preds, int n_pred) {
   using clock = std::chrono::steady_clock;
-  const volatile int32_t *ids = e->h_ids, *pred = e->h_pred;
+  const volatile int32_t *ids = e->h_ids;
   auto ready = [&]() {
     bool r = true;
     for (int32_t i = 0; i < e->k; ++i) r = r && ids[i] >= 0;
-    for (int32_t i = 0; look && i < e->kp; ++i) r = r && pred[i] >= 0;
+    for (int j = 0; j < n_pred; ++j) {
+      const volatile int32_t *pred = preds[j];
+      for (int32_t i = 0; i < e->kp; ++i) r = r && pred[i] >= 0;
+    }
     return r;
   };
   clock::time_point next{};
@@ -131,12 +151,22 @@ int engine_wait_route(moe_engine *e, bool look) {
     if (now < next) continue;
     next = now + std::chrono::milliseconds(1);
     const hipError_t q = hipStreamQuery(e->compute);
-    if (q == hipErrorNotReady) continue;
-    if (q != hipSuccess) return hip_fail(q, "router launch");
+    const hipError_t ql = hipStreamQuery(e->look);
+    if (q != hipSuccess && q != hipErrorNotReady) return hip_fail(q, "router launch");
+    if (ql != hipSuccess && ql != hipErrorNotReady) return hip_fail(ql, "lookahead launch");
+    if (q == hipErrorNotReady || ql == hipErrorNotReady) continue;
     if (!ready()) return fail(MOE_ERR_INVALID, "router finished without writing its ids");
   }
   std::atomic_thread_fence(std::memory_order_acquire);
   return MOE_OK;
+}
+
+// Unique predicted ids, ascending (np.unique of the prediction).
+std::vector<int32_t> engine_unique(const int32_t *pred, int32_t n) {
+  std::vector<int32_t> up(pred, pred + n);
+  std::sort(up.begin(), up.end());
+  up.erase(std::unique(up.begin(), up.end()), up.end());
+  return up;
 }
 
 int engine_fill(moe_engine *e, int32_t layer, const int32_t *experts, const int32_t *slots,
@@ -191,6 +221,8 @@ int moe_engine_create(const moe_pool_view *pool, const moe_geom *g, int32_t n_la
   e->record_bytes = record_bytes;
   e->n_records = n_records;
   e->L = n_layers;
+  e->pred_for.resize(n_layers);
+  e->pred_set.assign(n_layers, 0);
   e->E = E;
   e->k = k;
   e->kp = k_pred;
@@ -205,6 +237,9 @@ int moe_engine_create(const moe_pool_view *pool, const moe_geom *g, int32_t n_la
   };
   dmalloc(reinterpret_cast<void **>(&e->d_scores), 256);
   dmalloc(&e->d_route_ws, e->route_ws_bytes);
+  dmalloc(reinterpret_cast<void **>(&e->d_idsx), 256);
+  dmalloc(reinterpret_cast<void **>(&e->d_scoresx), 256);
+  dmalloc(&e->d_route_wsx, e->route_ws_bytes);
   dmalloc(&e->d_ffn_ws, e->ffn_ws_bytes);
   auto shared = [&](int32_t **h, int32_t **k) {
     if (err == hipSuccess)
@@ -215,6 +250,9 @@ int moe_engine_create(const moe_pool_view *pool, const moe_geom *g, int32_t n_la
   };
   shared(&e->h_ids, &e->k_ids);
   shared(&e->h_pred, &e->k_pred);
+  for (int i = 0; i < kEngineMaxDepths - 1; ++i) shared(&e->h_predx[i], &e->k_predx[i]);
+  if (err == hipSuccess) err = hipStreamCreateWithFlags(&e->look, hipStreamNonBlocking);
+  if (err == hipSuccess) err = hipEventCreateWithFlags(&e->x_ready, hipEventDisableTiming);
   if (err != hipSuccess) {
     moe_engine_destroy(e);
     return hip_fail(err, "engine buffers");
@@ -227,6 +265,7 @@ int moe_engine_destroy(moe_engine *e) {
   if (!e) return MOE_OK;
   if (e->compute) (void)hipStreamSynchronize(e->compute);
   if (e->side) (void)hipStreamSynchronize(e->side);
+  if (e->look) (void)hipStreamSynchronize(e->look);
   std::vector<hipEvent_t> evs = e->free_events;
   for (const auto &kv : e->pending) evs.push_back(kv.second);
   std::sort(evs.begin(), evs.end());
@@ -235,61 +274,121 @@ int moe_engine_destroy(moe_engine *e) {
   (void)hipFree(e->d_scores);
   (void)hipFree(e->d_route_ws);
   (void)hipFree(e->d_ffn_ws);
+  (void)hipFree(e->d_idsx);
+  (void)hipFree(e->d_scoresx);
+  (void)hipFree(e->d_route_wsx);
   (void)hipHostFree(e->h_ids);
   (void)hipHostFree(e->h_pred);
+  for (int i = 0; i < kEngineMaxDepths - 1; ++i) (void)hipHostFree(e->h_predx[i]);
+  if (e->x_ready) (void)hipEventDestroy(e->x_ready);
+  if (e->look) (void)hipStreamDestroy(e->look);
   delete e;
   return MOE_OK;
 }
 
-int moe_engine_layer(moe_engine *e, int32_t layer, const uint16_t *x, const uint16_t *W,
-                     const uint16_t *bias, int32_t mode, int32_t renorm,
-                     const uint16_t *W_next, const uint16_t *bias_next, uint16_t *y) {
+int moe_engine_layer_depths(moe_engine *e, int32_t layer, const uint16_t *x,
+                            const uint16_t *W, const uint16_t *bias, int32_t mode,
+                            int32_t renorm, const int32_t *depths, int32_t n_depths,
+                            const uint16_t *const *W_look, const uint16_t *const *bias_look,
+                            uint16_t *y) {
   if (!e) return fail(MOE_ERR_INVALID, "engine is NULL");
   if (layer < 0 || layer >= e->L) return fail(MOE_ERR_INVALID, "layer %d outside [0, %d)", layer, e->L);
   if (!x || !W || !y) return fail(MOE_ERR_INVALID, "NULL x/W/y");
-  const bool look = W_next != nullptr && layer + 1 < e->L;
-  // 1. route + lookahead, outputs into pinned memory reset to -1
+  if (n_depths < 0 || n_depths > kEngineMaxDepths || (n_depths > 0 && (!depths || !W_look)))
+    return fail(MOE_ERR_INVALID, "n_depths=%d outside [0, %d] or NULL depths/W_look", n_depths,
+                kEngineMaxDepths);
+  for (int32_t j = 0; j < n_depths; ++j)
+    if (depths[j] <= 0) return fail(MOE_ERR_INVALID, "depth %d is not positive", depths[j]);
+  // the depths that name a layer of the stack and come with a router
+  bool on[kEngineMaxDepths] = {};
+  for (int32_t j = 0; j < n_depths; ++j)
+    on[j] = W_look[j] != nullptr && (int64_t)layer + depths[j] < e->L;
+  const bool look = n_depths > 0 && on[0];
+  auto bias_of = [&](int32_t j) { return bias_look ? bias_look[j] : nullptr; };
+  // 1. route + the first lookahead, outputs into pinned memory reset to -1;
+  // further depths on the lookahead stream, ordered after x
   for (int32_t i = 0; i < e->k; ++i) e->h_ids[i] = -1;
   for (int32_t i = 0; look && i < e->kp; ++i) e->h_pred[i] = -1;
+  const int32_t *preds[kEngineMaxDepths];
+  int n_pred = 0;
+  if (look) preds[n_pred++] = e->h_pred;
+  bool further = false;
+  for (int32_t j = 1; j < n_depths; ++j) {
+    if (!on[j]) continue;
+    for (int32_t i = 0; i < e->kp; ++i) e->h_predx[j - 1][i] = -1;
+    preds[n_pred++] = e->h_predx[j - 1];
+    further = true;
+  }
   std::atomic_thread_fence(std::memory_order_release);
+  if (further) {
+    MOE_HIP(hipEventRecord(e->x_ready, e->compute));
+    MOE_HIP(hipStreamWaitEvent(e->look, e->x_ready, 0));
+  }
   int rc = moe_route(x, 1, e->geom.d_model, W, bias, e->E, mode, renorm, e->k, e->k_ids,
-                     e->d_scores, look ? W_next : nullptr, look ? bias_next : nullptr, e->kp,
+                     e->d_scores, look ? W_look[0] : nullptr, look ? bias_of(0) : nullptr, e->kp,
                      look ? e->k_pred : nullptr, nullptr, nullptr, nullptr, e->d_route_ws,
                      e->route_ws_bytes, e->compute);
   if (rc) return rc;
+  // a further depth's ids: top-kp of its router's logits (top_k_indices,
+  // engine_v3.py:476-483), the lookahead rows of a route launch on that router
+  for (int32_t j = 1; j < n_depths; ++j) {
+    if (!on[j]) continue;
+    rc = moe_route(x, 1, e->geom.d_model, W_look[j], bias_of(j), e->E, MOE_ROUTE_TOPK_SOFTMAX, 0,
+                   1, e->d_idsx, e->d_scoresx, W_look[j], bias_of(j), e->kp, e->k_predx[j - 1],
+                   nullptr, nullptr, nullptr, e->d_route_wsx, e->route_ws_bytes, e->look);
+    if (rc) return rc;
+  }
   // 2. one host synchronisation for routing and speculation
-  rc = engine_wait_route(e, look);
+  rc = engine_wait_route(e, preds, n_pred);
   if (rc) return rc;
-  // 3. recall of the prediction made for this layer
-  if (e->last_pred_layer == layer) {
+  // 3. recall of the prediction made for this layer (first depth only, as
+  // the reference's _PRED)
+  if (e->pred_set[layer]) {
     int32_t hit = 0;
     for (int32_t i = 0; i < e->k; ++i)
-      for (int32_t p : e->last_pred) hit += p == e->h_ids[i];
+      for (int32_t p : e->pred_for[layer]) hit += p == e->h_ids[i];
     e->recall_hit += hit;
     e->recall_total += e->k;
+    e->pred_set[layer] = 0;
   }
   rc = engine_poll(e);
   if (rc) return rc;
-  // 4. prefetch of layer + 1 (unique predicted ids, ascending, as np.unique)
-  if (look) {
-    std::vector<int32_t> up(e->h_pred, e->h_pred + e->kp);
-    std::sort(up.begin(), up.end());
-    up.erase(std::unique(up.begin(), up.end()), up.end());
-    e->last_pred = up;
-    e->last_pred_layer = layer + 1;
-    int32_t slots[kEngineMaxPred], exps[kEngineMaxPred], bailed = 0;
-    const int n = moe_policy_prefetch(e->policy, layer + 1, up.data(), (int32_t)up.size(), slots,
-                                      exps, &bailed);
-    if (n < 0) return fail(n, "policy prefetch failed");
-    if (n > 0) {
-      rc = engine_fill(e, layer + 1, exps, slots, n, e->side);
-      if (rc) return rc;
-      hipEvent_t ev;
-      rc = engine_event(e, &ev);
-      if (rc) return rc;
-      MOE_HIP(hipEventRecord(ev, e->side));
-      for (int i = 0; i < n; ++i) e->pending[engine_key(e, layer + 1, exps[i])] = ev;
+  // 4. prefetch of each depth's target layer in the list's order (unique
+  // predicted ids, ascending, as np.unique); the first depth's copies now,
+  // the further depths' after the expert block's launch
+  struct Deferred {
+    int32_t tgt, n;
+    int32_t slots[kEngineMaxPred], exps[kEngineMaxPred];
+  };
+  Deferred later[kEngineMaxDepths - 1];
+  int n_later = 0;
+  for (int32_t j = 0, pj = 0; j < n_depths; ++j) {
+    if (!on[j] || (j == 0 && !look)) continue;
+    const std::vector<int32_t> up = engine_unique(preds[pj++], e->kp);
+    const int32_t tgt = layer + depths[j];
+    if (j == 0) {
+      e->pred_for[tgt] = up;
+      e->pred_set[tgt] = 1;
     }
+    Deferred &d = later[n_later];
+    int32_t bailed = 0;
+    const int n = moe_policy_prefetch(e->policy, tgt, up.data(), (int32_t)up.size(), d.slots,
+                                      d.exps, &bailed);
+    if (n < 0) return fail(n, "policy prefetch failed");
+    if (n == 0) continue;
+    if (j > 0) {
+      d.tgt = tgt;
+      d.n = n;
+      ++n_later;
+      continue;
+    }
+    rc = engine_fill(e, tgt, d.exps, d.slots, n, e->side);
+    if (rc) return rc;
+    hipEvent_t ev;
+    rc = engine_event(e, &ev);
+    if (rc) return rc;
+    MOE_HIP(hipEventRecord(ev, e->side));
+    for (int i = 0; i < n; ++i) e->pending[engine_key(e, tgt, d.exps[i])] = ev;
   }
   // 5. acquire: misses on the compute stream, pending prefetches as waits
   int32_t miss_idx[MOE_MAX_TOPK], wait_idx[MOE_MAX_TOPK], n_miss = 0, n_wait = 0;
@@ -326,7 +425,26 @@ int moe_engine_layer(moe_engine *e, int32_t layer, const uint16_t *x, const uint
                          static_cast<uint16_t *>(e->d_ffn_ws), y, nullptr, e->geom.act,
                          e->geom.alpha, e->geom.limit, e->compute);
   MOE_HIP(hipGetLastError());
+  // 7. the further depths' prefetch copies, one event per depth
+  for (int i = 0; i < n_later; ++i) {
+    const Deferred &d = later[i];
+    rc = engine_fill(e, d.tgt, d.exps, d.slots, d.n, e->side);
+    if (rc) return rc;
+    hipEvent_t ev;
+    rc = engine_event(e, &ev);
+    if (rc) return rc;
+    MOE_HIP(hipEventRecord(ev, e->side));
+    for (int k = 0; k < d.n; ++k) e->pending[engine_key(e, d.tgt, d.exps[k])] = ev;
+  }
   return MOE_OK;
+}
+
+int moe_engine_layer(moe_engine *e, int32_t layer, const uint16_t *x, const uint16_t *W,
+                     const uint16_t *bias, int32_t mode, int32_t renorm,
+                     const uint16_t *W_next, const uint16_t *bias_next, uint16_t *y) {
+  const int32_t depth = 1;
+  return moe_engine_layer_depths(e, layer, x, W, bias, mode, renorm, &depth, 1, &W_next,
+                                 &bias_next, y);
 }
 
 int moe_engine_counters(const moe_engine *e, int64_t *out) {

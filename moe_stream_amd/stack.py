@@ -335,12 +335,14 @@ class StreamingStack:
                  seed: int = synth.SEED_BASE + 2, zipf_s: float | None = 1.1,
                  router_bias: bool = False, widen: int = 1, host_store=None,
                  evict: str | None = None, native: bool = False,
-                 pool_layout: str = "records"):
+                 pool_layout: str = "records", depths=(1,)):
         """native: run each layer's engine loop in the library
         (moe_engine_layer) instead of MoEBlock.streaming_call; same policy,
         fills and kernels, no Python frame between a layer's steps.
         pool_layout: "records" (a fill is one copy-engine copy per record) or
-        "components" (copy-kernel fills)."""
+        "components" (copy-kernel fills).
+        depths: the prefetch depths (the reference's PF_DEPTH list,
+        engine_v3.py:61), each layer L's hidden state predicting layer L+d."""
         from .block import MoEBlock
         from .pool import ExpertPool
         self.geom = geom
@@ -350,15 +352,19 @@ class StreamingStack:
         self.device = _norm_device(device)
         self.store = host_store if host_store is not None else \
             synth.make_host_store(geom, n_layers * self.E, self.device, seed)
+        self.depths = tuple(int(d) for d in depths)
+        if not self.depths or min(self.depths) <= 0 or len(self.depths) > 4:
+            raise ValueError(f"depths {depths!r}: 1 to 4 positive layer offsets")
         self.pool = ExpertPool(geom, n_slots, store=self.store, device=self.device, evict=evict,
-                               widen=widen, n_layers=n_layers, layout=pool_layout)
+                               widen=widen, n_layers=n_layers, layout=pool_layout,
+                               depths=self.depths)
         self.W, self.bias, self.logpop = routers(geom, n_layers, self.device, seed,
                                                  zipf_s, router_bias)
         self.blocks = []
         for Lx in range(n_layers):
             self.blocks.append(MoEBlock(Lx, geom, self.pool, self.W[Lx],
                                         None if self.bias is None else self.bias[Lx],
-                                        self.blocks, widen=widen))
+                                        self.blocks, depths=self.depths, widen=widen))
         self.native = native
         self._engine = None
         if native:
@@ -408,16 +414,43 @@ class StreamingStack:
                            for Lx in range(L)]
         return self._largs
 
+    def _depth_args(self):
+        """Per layer: (router, router bias, depths, routers and biases of
+        the target layers) for moe_engine_layer_depths; a target past the
+        last layer has a NULL router."""
+        if getattr(self, "_dargs", None) is None:
+            W, b, L, n = self.W, self.bias, self.L, len(self.depths)
+            ptr = lambda t: None if t is None else t.data_ptr()
+            depths = (C.c_int32 * n)(*self.depths)
+            self._dargs = []
+            for Lx in range(L):
+                tg = [Lx + d for d in self.depths]
+                wl = (C.c_void_p * n)(*[W[t].data_ptr() if t < L else None for t in tg])
+                bl = None if b is None else \
+                    (C.c_void_p * n)(*[b[t].data_ptr() if t < L else None for t in tg])
+                self._dargs.append((W[Lx].data_ptr(), ptr(None if b is None else b[Lx]),
+                                    depths, wl, bl))
+        return self._dargs
+
     def _token_native(self, x_tok, out):
         assert x_tok.is_contiguous() and out.is_contiguous()
         assert x_tok.dtype == out.dtype == torch.bfloat16
         assert x_tok.shape == out.shape == (self.L, self.geom.d_model)
         step = self.geom.d_model * 2
-        layer, eng, g = _lib.lib().moe_engine_layer, self._engine, self.geom
+        eng, g = self._engine, self.geom
         mode, renorm = g.routing, int(g.norm_topk_prob)
         x0, y0 = x_tok.data_ptr(), out.data_ptr()
-        for Lx, (w, b, wn, bn) in enumerate(self._layer_args()):
-            rc = layer(eng, Lx, x0 + Lx * step, w, b, mode, renorm, wn, bn, y0 + Lx * step)
+        if self.depths == (1,):
+            layer = _lib.lib().moe_engine_layer
+            for Lx, (w, b, wn, bn) in enumerate(self._layer_args()):
+                rc = layer(eng, Lx, x0 + Lx * step, w, b, mode, renorm, wn, bn, y0 + Lx * step)
+                if rc < 0:
+                    _lib.check(rc)
+            return out
+        layer, n = _lib.lib().moe_engine_layer_depths, len(self.depths)
+        for Lx, (w, b, depths, wl, bl) in enumerate(self._depth_args()):
+            rc = layer(eng, Lx, x0 + Lx * step, w, b, mode, renorm, depths, n, wl, bl,
+                       y0 + Lx * step)
             if rc < 0:
                 _lib.check(rc)
         return out

@@ -95,6 +95,37 @@ def test_native_engine_matches_python_loop(stacks):
     na.close()
 
 
+@pytest.mark.parametrize("depths", [(1, 2), (2, 1, 3)])
+def test_native_engine_depth_list_equals_resident_stack(stacks, depths):
+    """A list of prefetch depths (the reference's PF_DEPTH, engine_v3.py:61,
+    509-527) through the library's engine loop (moe_engine_layer_depths) and
+    through MoEBlock.streaming_call: outputs equal the HBM-resident stack's,
+    prefetches are issued, recall counts the first depth only."""
+    geom, dec, _, xs = stacks
+    na = StreamingStack(geom, L, 40, "cuda", seed=20260601, zipf_s=1.1, native=True,
+                        depths=depths)
+    py = StreamingStack(geom, L, 40, "cuda", seed=20260601, zipf_s=1.1, depths=depths)
+    one = StreamingStack(geom, L, 40, "cuda", seed=20260601, zipf_s=1.1, native=True)
+    for t in range(xs.shape[0]):
+        dec.run_token(xs[t], use_graph=False)
+        a = na.token(xs[t])
+        b = py.token(xs[t])
+        one.token(xs[t])
+        torch.cuda.synchronize()
+        assert torch.equal(a, dec.y), t
+        assert torch.equal(b, dec.y), t
+    s, s1 = na.pool.stats(), one.pool.stats()
+    c = na.engine_counters()
+    assert s["total"] == xs.shape[0] * L * 8
+    assert s["miss"] + s["prefetch"] + s["cache"] == s["total"]
+    assert c["bytes_read"] == (s["issued"] + s["miss"]) * geom.record_bytes
+    # the first depth's target layers are the only ones counted for recall
+    assert c["recall_total"] == xs.shape[0] * (L - depths[0]) * 8
+    assert s["issued"] > 0 and s1["issued"] > 0
+    na.close()
+    one.close()
+
+
 def test_native_engine_gptoss_equals_resident_stack():
     """The engine loop on the gpt-oss geometry (top-4, projection biases,
     clamped SwiGLU, biased router, top-k then softmax): the decode kernels
