@@ -16,8 +16,9 @@ wait, and counts as a prefetch hit.
 
 Parity status: pinned by hand-derived known answers on tiny pools (free list
 popped from the end, stride-7919 sampling order, young-entry protection,
-pinned/pending exclusion, exhaustion) and by invariants on random traces
-(tests/test_oracle_policy.py).
+pinned/pending exclusion, exhaustion), by invariants on random traces, and
+against `prefetch_simulator` below, a restatement of the reference's own
+second model of the same pool (tests/test_policy.py).
 """
 from __future__ import annotations
 
@@ -175,3 +176,81 @@ class PolicyOracle:
         return dict(total=tot, prefetch=self.n_prefetch_hit,
                     cache=self.n_cache_hit, miss=self.n_miss,
                     bail=self.n_prefetch_bail, issued=self.n_prefetch_issued)
+
+
+def prefetch_simulator(true, pred, cap: int, mode: str = "lfu", window: int = 24):
+    """The reference's prefetch-aware pool simulator (scratchpad/prefetch_sim.py:
+    21-94), restated: a second model of ExpertPool written by the reference's
+    author, used to cross-check the restatement above.
+
+    true, pred: integer arrays [L, T, k] and [L, T, kp] of expert ids.  Per
+    token and layer l: the pin set starts empty; each routed expert of layer
+    l is looked up (a hit if resident, else admitted through the sampled
+    eviction), recorded as a use and pinned; then every predicted expert of
+    layer l + 1 that is not resident is admitted at once (reads complete
+    instantly: nothing is ever pending).  Eviction is engine_v3.py's: stride
+    7919 from clock % cap over at most SAMPLE unpinned candidates, base
+    0 / last use / use count by mode, +2^30 for entries admitted fewer than
+    `window` admissions ago; admission is not a use.
+    Returns (admissions, hits, accesses)."""
+    L, T = len(true), len(true[0])
+    E = 1 + max(max(int(e) for row in true for ids in row for e in ids),
+                max(int(e) for row in pred for ids in row for e in ids))
+    key_at = [None] * cap
+    where, uses, born, last = {}, defaultdict(int), {}, {}
+    free = list(range(cap))
+    clock = tick = admitted = hits = accesses = 0
+    pins = set()
+
+    def admit(key):
+        nonlocal clock, admitted
+        clock += 1
+        admitted += 1
+        if free:
+            slot = free.pop()
+        else:
+            best, victim, looked = None, None, 0
+            for j in range(cap):
+                s = (clock % cap + j * STRIDE) % cap
+                k = key_at[s]
+                if k is None or s in pins:
+                    continue
+                base = {"asis": 0, "lru": last.get(k, 0)}.get(mode, uses.get(k, 0))
+                score = base + (YOUNG if clock - born.get(k, 0) < window else 0)
+                if best is None or score < best:
+                    best, victim = score, s
+                looked += 1
+                if looked >= SAMPLE and best < YOUNG:
+                    break
+            if victim is None:   # every resident entry pinned: first unpinned slot
+                victim = next(s for s in range(cap) if s not in pins)
+            old = key_at[victim]
+            del where[old]
+            for d in (born, last, uses):
+                d.pop(old, None)
+            slot = victim
+        key_at[slot] = key
+        where[key] = slot
+        born[key] = clock
+        return slot
+
+    for t in range(T):
+        for l in range(L):
+            pins = set()
+            for e in true[l][t]:
+                key = l * E + int(e)
+                accesses += 1
+                if key in where:
+                    hits += 1
+                else:
+                    admit(key)
+                tick += 1
+                last[key] = tick
+                uses[key] += 1
+                pins.add(where[key])
+            if l + 1 < L:
+                for e in pred[l + 1][t]:
+                    key = (l + 1) * E + int(e)
+                    if key not in where:
+                        admit(key)
+    return admitted, hits, accesses

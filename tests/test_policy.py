@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 
 from moe_stream_amd.policy import NativePolicy, PoolExhausted
-from oracle.policy import PolicyOracle
+from oracle.policy import PolicyOracle, prefetch_simulator
 from oracle.policy import PoolExhausted as OracleExhausted
 
 
@@ -146,3 +146,62 @@ def test_native_policy_rejects_bad_keys():
         n.acquire(2, [0])
     with pytest.raises(Exception):
         n.prefetch(0, [3])
+
+
+# ------------------------------- against the reference's pool simulator --
+def _zipf_trace(rng, L, T, E, k, kp, recall):
+    """Routed ids [L, T, k] from a Zipf-like popularity, and predictions
+    [L, T, kp] that keep each routed id with probability `recall` and fill
+    the rest with popular ids (as the lookahead does)."""
+    pop = 1.0 / np.arange(1, E + 1) ** 1.1
+    pop /= pop.sum()
+    true = np.zeros((L, T, k), dtype=np.int64)
+    pred = np.zeros((L, T, kp), dtype=np.int64)
+    for l in range(L):
+        perm = rng.permutation(E)      # each layer its own popular experts
+        for t in range(T):
+            ids = perm[rng.choice(E, size=k, replace=False, p=pop)]
+            true[l, t] = ids
+            keep = [int(e) for e in ids if rng.random() < recall]
+            rest = [int(e) for e in perm[rng.choice(E, size=2 * kp, replace=False, p=pop)]
+                    if int(e) not in keep]
+            pred[l, t] = (keep + rest)[:kp]
+    return true, pred
+
+
+@pytest.mark.parametrize("evict", ["lfu", "lru", "asis"])
+@pytest.mark.parametrize("cap", [40, 96, 300])
+def test_policy_matches_reference_pool_simulator(evict, cap):
+    """Driven in the simulator's order (per token and layer: pins cleared,
+    acquire of the routed ids, then prefetch of the next layer's predicted
+    ids with each fill completed at once), the native policy and the oracle
+    admit exactly as many entries and hit exactly as often as the
+    reference's second model of the pool (scratchpad/prefetch_sim.py:21-94),
+    for every eviction mode and pool sizes from tight to roomy."""
+    rng = np.random.default_rng(cap * 7 + len(evict))
+    L, T, E, k, kp = 6, 40, 64, 8, 8
+    true, pred = _zipf_trace(rng, L, T, E, k, kp, recall=0.8)
+    want = prefetch_simulator(true, pred, cap, evict)
+    n = NativePolicy(cap, L, E, evict=evict)
+    o = PolicyOracle(cap, evict=evict)
+    for t in range(T):
+        for l in range(L):
+            n.acquire(l, [])           # the simulator's pin set starts empty
+            o.acquire(l, [])
+            n.acquire(l, true[l, t])
+            o.acquire(l, true[l, t].tolist())
+            if l + 1 < L:
+                for e in pred[l + 1, t]:   # one at a time, each read done at once
+                    _, fe, bailed = n.prefetch(l + 1, [int(e)])
+                    assert not bailed
+                    for x in fe:
+                        n.complete(l + 1, int(x))
+                    o.prefetch(l + 1, [int(e)])
+                    if (l + 1, int(e)) in o.pending:
+                        o.complete((l + 1, int(e)))
+    sn, so = n.stats(), o.stats()
+    admitted, hits, accesses = want
+    assert sn["total"] == so["total"] == accesses == L * T * k
+    assert sn["issued"] + sn["miss"] == so["issued"] + so["miss"] == admitted
+    assert sn["prefetch"] + sn["cache"] == so["prefetch"] + so["cache"] == hits
+    assert 0 < hits < accesses
