@@ -390,41 +390,48 @@ int moe_engine_layer_depths(moe_engine *e, int32_t layer, const uint16_t *x,
     MOE_HIP(hipEventRecord(ev, e->side));
     for (int i = 0; i < n; ++i) e->pending[engine_key(e, tgt, d.exps[i])] = ev;
   }
-  // 5. acquire: misses on the compute stream, pending prefetches as waits
-  int32_t miss_idx[MOE_MAX_TOPK], wait_idx[MOE_MAX_TOPK], n_miss = 0, n_wait = 0;
-  rc = moe_policy_acquire(e->policy, layer, e->h_ids, e->k, e->h_refs, miss_idx, &n_miss,
-                          wait_idx, &n_wait);
-  if (rc) return fail(rc, rc == MOE_ERR_EXHAUSTED ? "pool exhausted: every slot pinned or pending"
-                                                  : "policy acquire failed");
-  if (n_miss > 0) {
-    int32_t exps[MOE_MAX_TOPK], slots[MOE_MAX_TOPK];
-    for (int32_t i = 0; i < n_miss; ++i) {
-      exps[i] = e->h_ids[miss_idx[i]];
-      slots[i] = e->h_refs[miss_idx[i]];
+  // 5-6 run as one step whose result is returned after the further depths'
+  // copies are issued: the policy already counts those prefetches as
+  // pending, so they are issued (with their events) whatever happens here
+  auto block = [&]() -> int {
+    // 5. acquire: misses on the compute stream, pending prefetches as waits
+    int32_t miss_idx[MOE_MAX_TOPK], wait_idx[MOE_MAX_TOPK], n_miss = 0, n_wait = 0;
+    rc = moe_policy_acquire(e->policy, layer, e->h_ids, e->k, e->h_refs, miss_idx, &n_miss,
+                            wait_idx, &n_wait);
+    if (rc) return fail(rc, rc == MOE_ERR_EXHAUSTED ? "pool exhausted: every slot pinned or pending"
+                                                    : "policy acquire failed");
+    if (n_miss > 0) {
+      int32_t exps[MOE_MAX_TOPK], slots[MOE_MAX_TOPK];
+      for (int32_t i = 0; i < n_miss; ++i) {
+        exps[i] = e->h_ids[miss_idx[i]];
+        slots[i] = e->h_refs[miss_idx[i]];
+      }
+      rc = engine_fill(e, layer, exps, slots, n_miss, e->compute);
+      if (rc) return rc;
+      e->bytes_exposed += (int64_t)n_miss * e->record_bytes;
     }
-    rc = engine_fill(e, layer, exps, slots, n_miss, e->compute);
-    if (rc) return rc;
-    e->bytes_exposed += (int64_t)n_miss * e->record_bytes;
-  }
-  for (int32_t w = 0; w < n_wait; ++w) {
-    const auto it = e->pending.find(engine_key(e, layer, e->h_ids[wait_idx[w]]));
-    if (it == e->pending.end()) continue;
-    MOE_HIP(hipStreamWaitEvent(e->compute, it->second, 0));
-    hipEvent_t ev = it->second;
-    e->pending.erase(it);
-    bool shared = false;
-    for (const auto &kv : e->pending) shared = shared || kv.second == ev;
-    if (!shared) e->free_events.push_back(ev);
-  }
-  // 6. the expert block, slot refs in the kernel arguments; pool arguments
-  // and launch shapes were checked at creation, x by the router
-  moe::RefList refs{};
-  for (int32_t i = 0; i < e->k; ++i) refs.inl[i] = e->h_refs[i];
-  (void)hipGetLastError();
-  moe::launch_ffn_decode(e->ffn, e->pa, refs, e->d_scores, x, 1, e->k,
-                         static_cast<uint16_t *>(e->d_ffn_ws), y, nullptr, e->geom.act,
-                         e->geom.alpha, e->geom.limit, e->compute);
-  MOE_HIP(hipGetLastError());
+    for (int32_t w = 0; w < n_wait; ++w) {
+      const auto it = e->pending.find(engine_key(e, layer, e->h_ids[wait_idx[w]]));
+      if (it == e->pending.end()) continue;
+      MOE_HIP(hipStreamWaitEvent(e->compute, it->second, 0));
+      hipEvent_t ev = it->second;
+      e->pending.erase(it);
+      bool shared = false;
+      for (const auto &kv : e->pending) shared = shared || kv.second == ev;
+      if (!shared) e->free_events.push_back(ev);
+    }
+    // 6. the expert block, slot refs in the kernel arguments; pool arguments
+    // and launch shapes were checked at creation, x by the router
+    moe::RefList refs{};
+    for (int32_t i = 0; i < e->k; ++i) refs.inl[i] = e->h_refs[i];
+    (void)hipGetLastError();
+    moe::launch_ffn_decode(e->ffn, e->pa, refs, e->d_scores, x, 1, e->k,
+                           static_cast<uint16_t *>(e->d_ffn_ws), y, nullptr, e->geom.act,
+                           e->geom.alpha, e->geom.limit, e->compute);
+    MOE_HIP(hipGetLastError());
+    return MOE_OK;
+  };
+  const int rc_block = block();
   // 7. the further depths' prefetch copies, one event per depth
   for (int i = 0; i < n_later; ++i) {
     const Deferred &d = later[i];
@@ -436,7 +443,7 @@ int moe_engine_layer_depths(moe_engine *e, int32_t layer, const uint16_t *x,
     MOE_HIP(hipEventRecord(ev, e->side));
     for (int k = 0; k < d.n; ++k) e->pending[engine_key(e, d.tgt, d.exps[k])] = ev;
   }
-  return MOE_OK;
+  return rc_block;
 }
 
 int moe_engine_layer(moe_engine *e, int32_t layer, const uint16_t *x, const uint16_t *W,
