@@ -502,8 +502,9 @@ def cpu_baseline(stack, xs, repeats, gpu_token=None):
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: the expert path at bs=1 does not shard "
-              "(see the sharding note in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: this build runs the expert path on one GPU "
+              "(a bs=1 decode stack is one independent replica per GPU); run with --gpus 1",
+              file=sys.stderr)
         sys.exit(2)
     if args.workload == "qwen3-prefill":
         return prefill(args)
