@@ -58,6 +58,14 @@ def test_argument_errors_are_reported_without_device_work():
     assert rc == _lib.MOE_ERR_INVALID and b"T=0" in lib.moe_last_error()
     with pytest.raises(_lib.MoeError):
         _lib.check(rc)
+    # the streaming engine's layer calls: a NULL engine is refused before any
+    # list is read (the depth-list checks follow the engine check)
+    depths = (C.c_int32 * 2)(1, 2)
+    rc = lib.moe_engine_layer_depths(None, 0, None, None, None, 0, 1, depths, 2, None, None,
+                                     None)
+    assert rc == _lib.MOE_ERR_INVALID and b"engine is NULL" in lib.moe_last_error()
+    rc = lib.moe_engine_layer(None, 0, None, None, None, 0, 1, None, None, None)
+    assert rc == _lib.MOE_ERR_INVALID and b"engine is NULL" in lib.moe_last_error()
 
 
 def test_workspace_sizes():
