@@ -144,6 +144,16 @@ def test_grouped_few_tokens_matches_oracle(qwen_layer, T):
     assert torch.equal(y, out)
 
 
+@pytest.mark.parametrize("T", [17, 33])
+def test_grouped_just_past_the_fused_router_matches_oracle(qwen_layer, T):
+    """One token past a whole number of 16-token router tiles: the MFMA
+    router's last tile holds a single real token (its other rows clamp to it
+    and are never stored), and the grouped block sees tiles of one row."""
+    x = bf16_randn((T, 2048), seed=20260070 + T)
+    bufs, _, _ = _grouped_vs_oracle(qwen_layer, x, f"qwen3 grouped T={T}")
+    _check_ids(qwen_layer, x, bufs)
+
+
 def test_grouped_gptoss_matches_oracle():
     layer = Layer(G.GPT_OSS_120B, 136, seed=20260047, router_bias=True)
     x = bf16_randn((40, 2880), seed=20260048)

@@ -126,15 +126,17 @@ def test_native_engine_depth_list_equals_resident_stack(stacks, depths):
     one.close()
 
 
-def test_native_engine_gptoss_equals_resident_stack():
+@pytest.mark.parametrize("depths", [(1,), (1, 2)])
+def test_native_engine_gptoss_equals_resident_stack(depths):
     """The engine loop on the gpt-oss geometry (top-4, projection biases,
     clamped SwiGLU, biased router, top-k then softmax): the decode kernels
     take the slot refs in their kernel arguments there too, and the outputs
-    are those of the HBM-resident stack bit for bit."""
-    geom, Lg = G.GPT_OSS_120B, 2
+    are those of the HBM-resident stack bit for bit, with one prefetch depth
+    and with a depth list (the further depth's router carries its bias)."""
+    geom, Lg = G.GPT_OSS_120B, 2 if len(depths) == 1 else 3
     dec = DecodeStack(geom, Lg, 256, "cuda", seed=20260611, zipf_s=None, router_bias=True)
     st = StreamingStack(geom, Lg, 16, "cuda", seed=20260611, zipf_s=None, router_bias=True,
-                        native=True)
+                        native=True, depths=depths)
     xs = synth.hidden_states(5, Lg, geom.d_model, "cuda", 20260612)
     for t in range(xs.shape[0]):
         dec.run_token(xs[t], use_graph=False)
