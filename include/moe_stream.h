@@ -334,6 +334,13 @@ int moe_policy_acquire(moe_policy *p, int32_t layer, const int32_t *experts,
                        int32_t n, int32_t *slots_out, int32_t *miss_idx,
                        int32_t *n_miss, int32_t *wait_idx, int32_t *n_wait);
 int moe_policy_complete(moe_policy *p, int32_t layer, int32_t expert);
+/* A pending prefetch whose fill was never issued (the caller's copy or event
+ * call failed): the key is unmapped and its slot returns to the free list,
+ * so a later acquire of it is a miss filled on demand rather than a wait on
+ * a fill that does not exist.  The reference's fill worker drops the pending
+ * entry on failure but keeps the mapping (engine_v3.py:292-301); this keeps
+ * a failed fill's slot from being read.  MOE_ERR_INVALID if not pending. */
+int moe_policy_cancel(moe_policy *p, int32_t layer, int32_t expert);
 /* slot of (layer, expert) or -1 */
 int moe_policy_lookup(const moe_policy *p, int32_t layer, int32_t expert);
 int moe_policy_is_pending(const moe_policy *p, int32_t layer, int32_t expert);

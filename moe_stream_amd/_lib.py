@@ -45,7 +45,7 @@ EXPORTS = (
     "moe_event_query", "moe_stream_wait_event", "moe_event_elapsed_ms",
     "moe_check_device_error",
     "moe_policy_create", "moe_policy_destroy", "moe_policy_prefetch",
-    "moe_policy_acquire", "moe_policy_complete", "moe_policy_lookup",
+    "moe_policy_acquire", "moe_policy_complete", "moe_policy_cancel", "moe_policy_lookup",
     "moe_policy_is_pending", "moe_policy_table", "moe_policy_stats",
     "moe_engine_create", "moe_engine_destroy", "moe_engine_layer", "moe_engine_layer_depths",
     "moe_engine_counters",
@@ -124,6 +124,7 @@ def _declare(lib):
         "moe_policy_prefetch": (C.c_int, [P, I32, P, I32, P, P, P]),
         "moe_policy_acquire": (C.c_int, [P, I32, P, I32, P, P, P, P, P]),
         "moe_policy_complete": (C.c_int, [P, I32, I32]),
+        "moe_policy_cancel": (C.c_int, [P, I32, I32]),
         "moe_policy_lookup": (C.c_int, [P, I32, I32]),
         "moe_policy_is_pending": (C.c_int, [P, I32, I32]),
         "moe_policy_table": (C.c_int, [P, P]),

@@ -362,6 +362,16 @@ int moe_engine_layer_depths(moe_engine *e, int32_t layer, const uint16_t *x,
   };
   Deferred later[kEngineMaxDepths - 1];
   int n_later = 0;
+  // Every prefetch the policy counts as pending gets a fill and an event, or
+  // is cancelled (unmapped, its slot freed) before an error returns: a
+  // pending entry without an event would let its target layer's acquire
+  // read a slot that was never filled.
+  auto cancel = [&](int32_t tgt, const int32_t *exps, int32_t n) {
+    for (int32_t i = 0; i < n; ++i) (void)moe_policy_cancel(e->policy, tgt, exps[i]);
+  };
+  auto cancel_later = [&](int from) {
+    for (int i = from; i < n_later; ++i) cancel(later[i].tgt, later[i].exps, later[i].n);
+  };
   for (int32_t j = 0, pj = 0; j < n_depths; ++j) {
     if (!on[j] || (j == 0 && !look)) continue;
     const std::vector<int32_t> up = engine_unique(preds[pj++], e->kp);
@@ -374,7 +384,10 @@ int moe_engine_layer_depths(moe_engine *e, int32_t layer, const uint16_t *x,
     int32_t bailed = 0;
     const int n = moe_policy_prefetch(e->policy, tgt, up.data(), (int32_t)up.size(), d.slots,
                                       d.exps, &bailed);
-    if (n < 0) return fail(n, "policy prefetch failed");
+    if (n < 0) {
+      cancel_later(0);
+      return fail(n, "policy prefetch failed");
+    }
     if (n == 0) continue;
     if (j > 0) {
       d.tgt = tgt;
@@ -382,12 +395,18 @@ int moe_engine_layer_depths(moe_engine *e, int32_t layer, const uint16_t *x,
       ++n_later;
       continue;
     }
+    hipEvent_t ev = nullptr;
     rc = engine_fill(e, tgt, d.exps, d.slots, n, e->side);
-    if (rc) return rc;
-    hipEvent_t ev;
-    rc = engine_event(e, &ev);
-    if (rc) return rc;
-    MOE_HIP(hipEventRecord(ev, e->side));
+    if (!rc) rc = engine_event(e, &ev);
+    if (!rc && hipEventRecord(ev, e->side) != hipSuccess) {
+      e->free_events.push_back(ev);
+      rc = fail(MOE_ERR_HIP, "hipEventRecord failed");
+    }
+    if (rc) {
+      cancel(tgt, d.exps, n);
+      cancel_later(0);
+      return rc;
+    }
     for (int i = 0; i < n; ++i) e->pending[engine_key(e, tgt, d.exps[i])] = ev;
   }
   // 5-6 run as one step whose result is returned after the further depths'
@@ -435,12 +454,17 @@ int moe_engine_layer_depths(moe_engine *e, int32_t layer, const uint16_t *x,
   // 7. the further depths' prefetch copies, one event per depth
   for (int i = 0; i < n_later; ++i) {
     const Deferred &d = later[i];
+    hipEvent_t ev = nullptr;
     rc = engine_fill(e, d.tgt, d.exps, d.slots, d.n, e->side);
-    if (rc) return rc;
-    hipEvent_t ev;
-    rc = engine_event(e, &ev);
-    if (rc) return rc;
-    MOE_HIP(hipEventRecord(ev, e->side));
+    if (!rc) rc = engine_event(e, &ev);
+    if (!rc && hipEventRecord(ev, e->side) != hipSuccess) {
+      e->free_events.push_back(ev);
+      rc = fail(MOE_ERR_HIP, "hipEventRecord failed");
+    }
+    if (rc) {
+      cancel_later(i);
+      return rc;
+    }
     for (int k = 0; k < d.n; ++k) e->pending[engine_key(e, d.tgt, d.exps[k])] = ev;
   }
   return rc_block;

@@ -44,6 +44,9 @@ void launch_ffn_decode(const FfnLaunch *L, const PoolArgs &pa,
 constexpr int kRouteMaxE = 128;
 constexpr int kRouteMaxT = 16;
 constexpr uint32_t kRouteSpinLimit = 1u << 20;   // polls before a router wait gives up
+// the router workspace's arrival word (32-bit index from the sequence word:
+// its own 128-byte line inside the 256-byte header); zero between launches
+constexpr int kRouteArrivedWord = 32;
 
 struct RouteArgs {
   const uint16_t *x;

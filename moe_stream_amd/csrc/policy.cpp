@@ -113,6 +113,21 @@ struct moe_policy {
     freq[k] += 1;
   }
 
+  void cancel(int32_t k) {
+    const int32_t slot = slot_of[k];
+    pending[k] = 0;
+    from_prefetch[k] = 0;
+    resident_born[k] = 0;
+    born[k] = 0;
+    last_use[k] = 0;
+    freq[k] = 0;
+    slot_of[k] = -1;
+    if (slot >= 0) {
+      key_of[slot] = -1;
+      free_list.push_back(slot);
+    }
+  }
+
   void complete(int32_t k) {
     if (pending[k]) {
       pending[k] = 0;
@@ -252,6 +267,14 @@ int moe_policy_acquire(moe_policy *p, int32_t layer, const int32_t *experts,
 int moe_policy_complete(moe_policy *p, int32_t layer, int32_t expert) {
   if (!p || bad_key(p, layer, expert)) return MOE_ERR_INVALID;
   p->complete(p->key(layer, expert));
+  return MOE_OK;
+}
+
+int moe_policy_cancel(moe_policy *p, int32_t layer, int32_t expert) {
+  if (!p || bad_key(p, layer, expert)) return MOE_ERR_INVALID;
+  const int32_t k = p->key(layer, expert);
+  if (!p->pending[k]) return MOE_ERR_INVALID;
+  p->cancel(k);
   return MOE_OK;
 }
 

@@ -230,6 +230,20 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   const uint32_t fl =
       __hip_atomic_load(a.counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
   const int nrows = a.E * (a.Wn ? 2 : 1);
+  const int ntask = a.T * (a.Wn ? 2 : 1);
+  // Workgroup 0's own tasks see every router row (task 0) and, when T < 4,
+  // every lookahead row (task T), so every writer of those has read the word
+  // before workgroup 0 advances it.  Otherwise -- lookahead rows with T >= 4,
+  // or workgroups that only rank (more tasks than rows) -- every workgroup
+  // counts itself in once it holds the word's value, and workgroup 0 waits
+  // for all of them before it advances the word.
+  const bool count_in = (int)gridDim.x > (nrows + 3) / 4 || (a.Wn != nullptr && a.T >= 4);
+  uint32_t *const arrived = a.counter + kRouteArrivedWord;
+  if (count_in && threadIdx.x == 0) {
+    uint32_t one = 1u;
+    asm volatile("" : "+v"(one) : "v"(fl));   // issued once the word's value is in
+    __hip_atomic_fetch_add(arrived, one, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   const int row = blockIdx.x * 4 + wave;
   if (row < nrows) router_rows<NIT>(a, row, lane, fl);
 
@@ -237,7 +251,6 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
   // workgroups.  The logits travel as flagged device-scope (sc1) entries,
   // coherent across XCDs without L2 writeback/invalidate; the poll of an
   // entry is its load.
-  const int ntask = a.T * (a.Wn ? 2 : 1);
   const int task = blockIdx.x * 4 + wave;
   if (task < ntask) {
     const TaskPre p = task_pre(a, task, lane);
@@ -247,14 +260,27 @@ __global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
                 l0, l1);
     select_task(a, task, lane, p, l0, l1);
   }
-  // Workgroup 0 advances the sequence word once its task 0 has seen all of
-  // token 0's router entries: every row writer read the word before writing
-  // them, so no writer of this launch can read the advanced value, and the
-  // other ranking waves polled with the same flag.
+  // Workgroup 0 advances the sequence word once no workgroup of this launch
+  // can still read it: its tasks have seen the entries of every writer (each
+  // read the word before writing), or, with count_in, every workgroup has
+  // counted itself in.  The arrival word is back at zero for the next launch.
   if (blockIdx.x != 0) return;
   __syncthreads();
-  if (threadIdx.x == 0)
+  if (threadIdx.x == 0) {
+    if (count_in) {
+      for (uint32_t spins = 0;
+           __hip_atomic_load(arrived, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < gridDim.x;
+           ++spins) {
+        if (spins > kRouteSpinLimit) {
+          flag_timeout();
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      __hip_atomic_store(arrived, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     __hip_atomic_store(a.counter, fl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -447,10 +447,16 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
   __shared__ int pred_cnt[2];          // predicted positions (<= K)
   __shared__ int pos_fix[K];           // position p runs a fix-up of this rank, or -1
   __shared__ int pos_rank[K];          // routing rank whose activations position p holds
-  __shared__ int staged[2];            // x and gate/up data ready (slot l & 1)
+  // monotonic: WAVES_U + 1 arrivals per layer (the gate/up waves' loads
+  // landed, x staged); layer l's meeting waits for (WAVES_U + 1) * (l + 1).
+  // A wave arrives for layer l + 1 only after layer l's meeting (gate/up
+  // waves) or after every wave's layer-l arrival on dsync (wave 7), so the
+  // count reaches that target exactly when layer l's arrivals are in.
+  __shared__ uint32_t staged;
   // layer flags (the value layer_flag(l) once the event of layer l happened)
   __shared__ uint32_t lstart;          // the layer boundary was seen (wave 7)
   __shared__ uint32_t routed;          // the routing and positions are known (wave 7)
+  __shared__ uint32_t looked;          // layer l+1's prediction is in pred_* (wave 6)
   __shared__ uint32_t hready[K];       // position p's activations polled (wave 4 + p)
   // monotonic counters
   __shared__ uint32_t dsync;           // 8 arrivals per layer: every wave is done with it
@@ -468,14 +474,11 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
   const int drow0 = dact ? wg * ROWS_D : 0;                                // down block
   {
     const uint32_t none = layer_flag(a, 0) - 1u;   // no flag of this launch
-    if (tid0 < 2) {
-      pred_cnt[tid0] = 0;   // layer 0 has no prediction
-      staged[tid0] = 0;
-    }
+    if (tid0 < 2) pred_cnt[tid0] = 0;   // layer 0 has no prediction
     if (tid0 < K) hready[tid0] = none;
     if (tid0 == 0) {
-      routed = lstart = none;
-      dsync = fsync = 0;
+      routed = lstart = looked = none;
+      dsync = fsync = staged = 0;
     }
   }
   __syncthreads();
@@ -502,14 +505,8 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
       // ---- gate/up of the predicted expert (loaded during the previous
       // layer): every wave's loads landed, x staged (wave 7), then the rows
       __builtin_amdgcn_s_waitcnt(0);
-      if (lane == 0) {
-        __hip_atomic_fetch_add(&staged[l & 1], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        while (__hip_atomic_load(&staged[l & 1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
-               C::WAVES_U + 1)
-          __builtin_amdgcn_s_sleep(1);
-      }
-      __builtin_amdgcn_wave_barrier();
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      lds_arrive(&staged);
+      lds_wait_count(&staged, (uint32_t)(C::WAVES_U + 1) * (uint32_t)(l + 1));
       if (uact && upos < pred_cnt[l & 1])
         ur.run(tid, act_l, asum_l, reinterpret_cast<const uint16_t *>(sbu_l),
                reinterpret_cast<const uint16_t *>(ubias_l), hpred + (size_t)upos * (F / 2),
@@ -517,7 +514,6 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
       if (wave == 0) trace_mark(a, l, TR_U_ARRIVED);
       lds_wait_flag(&routed, fl);
       if (wave == 0) trace_mark(a, l, TR_SELECTED);
-      if (tid == 0) staged[(l + 1) & 1] = 0;   // the next layer's meeting counter
       if (wg == 0 && tid < K) {
         KARG(ids)[(size_t)l * K + tid] = sel_id[tid];
         KARG(scores)[(size_t)l * K + tid] = sel_sc[tid];
@@ -567,6 +563,9 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
       // ---- gate/up loads of layer l+1's prediction, once this workgroup's
       // activation polls are done (loads queued ahead of them would delay
       // them); in flight through the down pass and the layer boundary
+      // (wave 6 publishes layer l+1's prediction under `looked`; it always
+      // does when there is a next layer)
+      if (has_next && uact) lds_wait_flag(&looked, fl);
       if (has_next && uact && upos < pred_cnt[(l + 1) & 1]) {
 #pragma unroll
         for (int p = 0; p < K; ++p) lds_wait_flag(&hready[p], fl);
@@ -651,6 +650,7 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
             pr[r1] = t1;
           }
           if (lane == 0) pred_cnt[(l + 1) & 1] = min(a.kp, K);
+          lds_set_flag(&looked, fl);
         }
         lds_wait_flag(&routed, fl);
       } else {
@@ -672,8 +672,7 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
             sm += dpp_f<kDppQuadXor2>(sm);
             if (i < XU4 && (i & 3) == 0) asum_l[i >> 2] = sm;
           }
-          if (lane == 0)
-            __hip_atomic_fetch_add(&staged[l & 1], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+          lds_arrive(&staged);
         }
         const int pcnt = pred_cnt[l & 1];
         const int e0 = lane, e1 = lane + 64;

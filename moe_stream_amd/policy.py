@@ -75,8 +75,21 @@ class NativePolicy:
     def complete(self, layer: int, expert: int):
         _lib.check(_lib.lib().moe_policy_complete(self._h, int(layer), int(expert)))
 
+    def cancel(self, layer: int, expert: int):
+        """Drop a pending prefetch whose fill was never issued: the key is
+        unmapped and its slot freed, so a later acquire refills it."""
+        _lib.check(_lib.lib().moe_policy_cancel(self._h, int(layer), int(expert)))
+
     def lookup(self, layer: int, expert: int) -> int:
-        return _lib.check(_lib.lib().moe_policy_lookup(self._h, int(layer), int(expert)))
+        """Slot of (layer, expert), or -1 when it is not resident (the C call
+        returns -1 for both an absent key and a bad one, so the range is
+        checked here)."""
+        layer, expert = int(layer), int(expert)
+        if not (0 <= layer < self.n_layers and 0 <= expert < self.n_experts):
+            raise _lib.MoeError(_lib.MOE_ERR_INVALID,
+                                f"key ({layer}, {expert}) outside [0, {self.n_layers}) x "
+                                f"[0, {self.n_experts})")
+        return int(_lib.lib().moe_policy_lookup(self._h, layer, expert))
 
     def is_pending(self, layer: int, expert: int) -> bool:
         return bool(_lib.check(_lib.lib().moe_policy_is_pending(self._h, int(layer), int(expert))))

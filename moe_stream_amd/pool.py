@@ -298,9 +298,16 @@ class ExpertPool(SlotPool):
         if len(slots):
             compute = torch.cuda.current_stream(self.device)
             self.side.wait_stream(compute)          # no refill under a running kernel
-            self._fill_tracked([self._record(layer, e) for e in exps], slots, self.side)
-            ev = torch.cuda.Event()
-            ev.record(self.side)
+            try:
+                self._fill_tracked([self._record(layer, e) for e in exps], slots, self.side)
+                ev = torch.cuda.Event()
+                ev.record(self.side)
+            except BaseException:
+                # no fill (or no event) for these: unmap them so a later
+                # acquire refills them instead of reading the slots
+                for e in exps:
+                    self.policy.cancel(layer, int(e))
+                raise
             for e in exps:
                 self.pending[(layer, int(e))] = ev
 

@@ -230,13 +230,22 @@ class DecodeStack:
     def token_persistent_checked(self, x_tok: torch.Tensor, stream=None):
         """One token by an ordinary launch, checked; if its grid was not
         resident at once, the token runs again by a cooperative launch.
-        Synchronises `stream` (one host round trip per token)."""
+        Synchronises `stream` (one host round trip per token).  The per-layer
+        miss counts (p_miss, accumulated by the kernel) of a launch that timed
+        out come from unfinished routing: they are restored before the retry."""
+        if not hasattr(self, "p_ws"):
+            self._persistent_buffers()
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        with torch.cuda.stream(s):
+            miss0 = self.p_miss.clone()
         self.token_persistent(x_tok, stream, ordinary=True)
         try:
             self.check_persistent(stream)
         except _lib.MoeError as e:
             if e.code != _lib.MOE_ERR_TIMEOUT:
                 raise
+            with torch.cuda.stream(s):
+                self.p_miss.copy_(miss0)
             self.token_persistent(x_tok, stream, ordinary=False)
             self.check_persistent(stream)
             return "cooperative"

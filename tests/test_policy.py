@@ -205,3 +205,40 @@ def test_policy_matches_reference_pool_simulator(evict, cap):
     assert sn["issued"] + sn["miss"] == so["issued"] + so["miss"] == admitted
     assert sn["prefetch"] + sn["cache"] == so["prefetch"] + so["cache"] == hits
     assert 0 < hits < accesses
+
+
+def test_cancel_unmaps_a_pending_prefetch():
+    """A prefetch whose fill was never issued is cancelled: the key is no
+    longer mapped or pending, its slot goes back to the free list (the next
+    allocation pops it from the end), and a later acquire of it is a miss
+    that refills it instead of a wait on a fill that does not exist."""
+    n = NativePolicy(4, 2, 8)
+    slots, exps, _ = n.prefetch(1, [5, 6])
+    assert list(exps) == [5, 6] and list(slots) == [3, 2]
+    n.cancel(1, 6)
+    assert not n.is_pending(1, 6) and n.lookup(1, 6) == -1
+    assert n.is_pending(1, 5) and n.lookup(1, 5) == 3
+    with pytest.raises(Exception):
+        n.cancel(1, 6)          # no longer pending
+    s, miss, wait = n.acquire(1, [6, 5])
+    assert list(miss) == [0] and list(wait) == [1]
+    assert s[0] == 2            # the freed slot, popped from the end again
+    assert s[1] == 3
+    st = n.stats()
+    assert st["miss"] == 1 and st["prefetch"] == 1
+
+
+def test_slot_of_view_absent_keys():
+    """pool.slot_of-style lookups of keys that are not resident give the
+    default / False / KeyError, not an error from the library."""
+    from moe_stream_amd.policy import SlotOf
+    n = NativePolicy(4, 2, 8)
+    v = SlotOf(n)
+    assert v.get((0, 3)) is None and v.get((0, 3), -7) == -7
+    assert (0, 3) not in v
+    with pytest.raises(KeyError):
+        v[(0, 3)]
+    n.acquire(0, [3])
+    assert (0, 3) in v and v[(0, 3)] == 3 and v.get((0, 3)) == 3
+    with pytest.raises(Exception):
+        n.lookup(2, 0)          # layer out of range
