@@ -17,7 +17,7 @@ import torch
 
 from . import _lib, ops
 from .geometry import Geometry
-from .pool import ExpertPool
+from .pool import ExpertPool, env_depths, env_widen
 
 
 def top_k_experts(x: torch.Tensor, W: torch.Tensor, k: int, norm: bool):
@@ -51,15 +51,18 @@ class MoEBlock:
 
     def __init__(self, layer: int, geom: Geometry, pool: ExpertPool,
                  router_W: torch.Tensor, router_bias: torch.Tensor | None,
-                 blocks: list, depths=(1,), widen: int = 1):
+                 blocks: list, depths=None, widen: int | None = None):
+        """depths / widen: the prefetch depths and speculation width; by
+        default PF_DEPTH and PF_WIDEN from the environment, as the
+        reference's module constants (engine_v3.py:61,84)."""
         self._layer = layer
         self.geom = geom
         self.pool = pool
         self.W = router_W
         self.bias = router_bias
         self.blocks = blocks
-        self.depths = tuple(depths)
-        self.widen = widen
+        self.depths = tuple(depths) if depths is not None else env_depths()
+        self.widen = int(widen) if widen is not None else env_widen()
         self.top_k = geom.top_k
         self.norm_topk_prob = geom.norm_topk_prob
         self.recall = []            # measured lookahead recall, as _RECALL

@@ -169,6 +169,33 @@ N_SLOTS = int(os.environ.get("PF_SLOTS", "3072"))
 N_WORKERS = int(os.environ.get("PF_WORKERS", "4"))
 
 
+def env_depths() -> tuple:
+    """Prefetch depths from PF_DEPTH, a comma-separated list (default "1";
+    engine_v3.py:61-62): the first is the depth whose recall is tracked and
+    which sizes the young-entry window."""
+    raw = os.environ.get("PF_DEPTH", "1")
+    try:
+        d = tuple(int(v) for v in raw.split(","))
+    except ValueError:
+        raise ValueError(f"PF_DEPTH={raw!r}: a comma-separated list of integers") from None
+    if not d or any(v <= 0 for v in d):
+        raise ValueError(f"PF_DEPTH={raw!r}: depths must be positive")
+    return d
+
+
+def env_widen() -> int:
+    """Speculation width from PF_WIDEN (default 1; engine_v3.py:84): the
+    lookahead fetches the top k * PF_WIDEN predicted experts."""
+    raw = os.environ.get("PF_WIDEN", "1")
+    try:
+        w = int(raw)
+    except ValueError:
+        raise ValueError(f"PF_WIDEN={raw!r}: an integer") from None
+    if w <= 0:
+        raise ValueError(f"PF_WIDEN={raw!r}: must be positive")
+    return w
+
+
 class ExpertPool(SlotPool):
     """Fixed pool of expert slots with stream-ordered fills and LFU eviction;
     the API of engine_v3.ExpertPool (engine_v3.py:125-464): `prefetch`,
@@ -183,8 +210,8 @@ class ExpertPool(SlotPool):
     host memory (HostStore) or HBM (uint8 [n_records, record_bytes])."""
 
     def __init__(self, model_dir, n_slots: int = N_SLOTS, n_workers: int = N_WORKERS,
-                 store=None, device="cuda", evict: str | None = None, depths=(1,),
-                 widen: int = 1, side_stream: torch.cuda.Stream | None = None,
+                 store=None, device="cuda", evict: str | None = None, depths=None,
+                 widen: int | None = None, side_stream: torch.cuda.Stream | None = None,
                  n_layers: int | None = None, layout: str = "records"):
         if isinstance(model_dir, Geometry):
             geom = model_dir
@@ -205,8 +232,9 @@ class ExpertPool(SlotPool):
         self.group_size = geom.group_size
         self.bits = geom.bits
         self.blob = geom.record_bytes
-        self.depths = tuple(depths)
-        self.widen = widen
+        # PF_DEPTH / PF_WIDEN from the environment unless given
+        self.depths = tuple(depths) if depths is not None else env_depths()
+        self.widen = int(widen) if widen is not None else env_widen()
         self.evict = (evict or os.environ.get("MOE_EVICT", "lfu")).lower()
         self.policy = NativePolicy(n_slots, self.n_layers, self.n_experts,
                                    evict=self.evict, depth=self.depths[0])
@@ -338,9 +366,10 @@ class ExpertPool(SlotPool):
         """int32 [n_layers, n_experts] slot table on the device (-1 = absent)."""
         return torch.from_numpy(self.policy.table()).to(self.device)
 
+    @property
     def busy_s(self) -> float:
         """Device seconds with at least one fill in flight (fills completed
-        so far)."""
+        so far); a float attribute, as the reference's (engine_v3.py:247)."""
         self._retire_fills()
         self._merge_spans(keep_last=True)
         return (self._busy_done_ms + sum(b - a for a, b in self._spans)) / 1e3
@@ -350,6 +379,6 @@ class ExpertPool(SlotPool):
         s = self.policy.stats()
         return dict(total=s["total"], prefetch=s["prefetch"], cache=s["cache"],
                     miss=s["miss"], blocked=self.t_blocked, gb=self.bytes_read / 2 ** 30,
-                    busy_s=self.busy_s(), depth=self.depth_sum / max(1, self.depth_n),
+                    busy_s=self.busy_s, depth=self.depth_sum / max(1, self.depth_n),
                     bail=s["bail"], issued=s["issued"],
                     exposed_gb=self.bytes_exposed / 2 ** 30)

@@ -27,11 +27,29 @@ def test_busy_time_is_the_union_of_fill_spans():
     assert o._spans == [(5.0, 9.0)] and abs(o._busy_done_ms - 3.0) < 1e-12
 
 
-def test_stats_keys_are_the_reference_keys():
-    import inspect
-    src = inspect.getsource(ExpertPool.stats)
-    for k in REFERENCE_STATS_KEYS:
-        assert f"{k}=" in src, k
+def test_stats_keys_and_values():
+    """stats() of a pool with no device state behind it (the native policy
+    is host-only; fills are stood in by their telemetry): the reference's
+    eleven keys, the policy's counters, and busy_s as a float attribute."""
+    from moe_stream_amd.policy import NativePolicy
+    p = object.__new__(ExpertPool)
+    p.policy = NativePolicy(8, 2, 4)
+    p.policy.acquire(0, [1, 2])              # 2 misses
+    p.policy.acquire(0, [1])                 # 1 cache hit
+    slots, exps, _ = p.policy.prefetch(1, [3])
+    p.policy.complete(1, 3)
+    p.policy.acquire(1, [3])                 # 1 prefetch hit
+    p.t_blocked, p.bytes_read, p.bytes_exposed = 0.25, 3 * 2 ** 30, 2 ** 29
+    p.depth_sum, p.depth_n = 6, 4
+    p._fills, p._spans, p._busy_done_ms = [], [(0.0, 2.0), (1.0, 4.0)], 1000.0
+    s = p.stats()
+    assert set(s) == REFERENCE_STATS_KEYS
+    assert (s["total"], s["prefetch"], s["cache"], s["miss"]) == (4, 1, 1, 2)
+    assert (s["issued"], s["bail"]) == (1, 0)
+    assert s["blocked"] == 0.25 and s["gb"] == 3.0 and s["exposed_gb"] == 0.5
+    assert s["depth"] == 1.5
+    assert abs(s["busy_s"] - 1.004) < 1e-12            # 1000 ms + the union [0, 4] ms
+    assert isinstance(p.busy_s, float) and abs(p.busy_s - 1.004) < 1e-12
 
 
 def test_record_layout_views_address_whole_records():
