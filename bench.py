@@ -24,6 +24,7 @@ import time
 import numpy as np
 
 HBM_PEAK_GBS = 8000.0   # MI355X HBM3E, 8 TB/s
+PCIE_PEAK_GBS = 64.0    # MI355X host interface, PCIe 5.0 x16, one direction
 
 
 def parse():
@@ -34,13 +35,14 @@ def parse():
     ap.add_argument("--tokens", type=int, default=64)
     ap.add_argument("--workload", default="qwen3-48l",
                     choices=["qwen3-48l", "gptoss-36l", "qwen3-prefill", "qwen3-stream",
-                             "qwen3-verify", "hbm-copy"],
+                             "qwen3-verify", "qwen3-layer", "hbm-copy"],
                     help="qwen3-prefill: 512 tokens per layer through the grouped "
                          "MFMA path; qwen3-verify: 8 tokens per layer (a speculative "
                          "verification step) through the expert block ops.ffn picks, "
                          "against the same tokens decoded one at a time; "
                          "qwen3-stream: 256 decode tokens over a 2048-slot "
-                         "pool fed from a pinned host store; hbm-copy: a 1 GiB device "
+                         "pool fed from a pinned host store; qwen3-layer: one layer at "
+                         "batch 1 (256-slot pool); hbm-copy: a 1 GiB device "
                          "copy, the achievable HBM rate and the known-size reference "
                          "for the FETCH_SIZE / WRITE_SIZE counters (secondary "
                          "measurements, not the headline)")
@@ -52,8 +54,15 @@ def parse():
                          "(checked after the timed steps; if a launch timed out the steps "
                          "are measured again with cooperative launches)")
     ap.add_argument("--cpu-repeats", type=int, default=96,
-                    help="timed layer-blocks of the CPU baseline (>= 60)")
+                    help="timed layer-blocks of the CPU baseline")
+    ap.add_argument("--cpu-layers", type=int, default=2,
+                    help="qwen3-prefill / qwen3-verify: timed many-token layer-blocks of "
+                         "the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="default workload: skip the other configurations (one layer, "
+                         "gpt-oss 36 layers, prefill, verification, streaming) that follow "
+                         "the headline in the same JSON line")
     ap.add_argument("--engine", default="native", choices=["native", "python"],
                     help="qwen3-stream: the per-layer engine loop in the library "
                          "(moe_engine_layer) or in Python (MoEBlock.streaming_call)")
@@ -114,6 +123,28 @@ def measured_traffic(workload, mode):
     except OSError:
         return None, None
     return (int(m.group(1)), name) if m else (None, None)
+
+
+def _prefill_roofline(flops, wbytes, block_s, block_ms):
+    """The grouped block's roofline against its binding floor: the larger of
+    the MFMA time (bf16 FLOPs at the dense peak) and the weight read (each
+    distinct routed expert's payload once, at the HBM peak)."""
+    t_mfma = flops / (MFMA_BF16_PEAK_TFS * 1e12)
+    t_hbm = wbytes / (HBM_PEAK_GBS * 1e9)
+    tflops = flops / block_s / 1e12
+    gbs = wbytes / block_s / 1e9
+    r = {"kernel": "expert block (group + gate/up + down + combine)", "traffic": None,
+         "floors_us_per_step": {"mfma": round(t_mfma * 1e6, 1), "hbm": round(t_hbm * 1e6, 1)},
+         "mfma_TFLOPs": round(tflops, 2), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFS, 4),
+         "weight_read_GBs": round(gbs, 1), "flops_per_step": flops,
+         "avg_block_us": round(float(block_ms.mean()) * 1e3, 2)}
+    if t_hbm >= t_mfma:
+        r.update(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                 frac=round(gbs / HBM_PEAK_GBS, 4))
+    else:
+        r.update(bound="mfma", achieved=round(tflops, 2), peak=MFMA_BF16_PEAK_TFS,
+                 unit="TFLOP/s", frac=round(tflops / MFMA_BF16_PEAK_TFS, 4))
+    return r
 
 
 def prefill(args):
@@ -190,15 +221,12 @@ def prefill(args):
                       "distinct_experts_per_layer": round(distinct / L, 1),
                       "max_pairs_per_expert": int(counts.max()),
                       "parallelism": "none (1 GPU)"},
-           "roofline": {"bound": "mfma", "kernel": "expert block (group + gate/up + "
-                        "down + combine)", "achieved": round(tflops, 2),
-                        "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s",
-                        "frac": round(tflops / MFMA_BF16_PEAK_TFS, 4), "traffic": None,
-                        "flops_per_step": flops,
-                        "avg_block_us": round(float(block_ms.mean()) * 1e3, 2)},
+           "roofline": _prefill_roofline(flops, wbytes, block_s, block_ms),
            "expert_weight_GBs": round(wbytes / block_s / 1e9, 1),
            "wall_s": round(wall, 3)}
-    print(json.dumps(out), flush=True)
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline_batch(stack, x_step, args.cpu_layers)
+    return out
 
 
 def verify(args):
@@ -265,8 +293,18 @@ def verify(args):
            "pairs_per_layer": T * stack.k,
            "distinct_experts_per_layer": round(float(np.mean(distinct)) / L, 2),
            "expert_bytes_per_verify": int(wbytes),
-           "expert_GBs": round(wbytes / (ver * 1e-3) / 1e9, 1)}
-    print(json.dumps(out), flush=True)
+           "expert_GBs": round(wbytes / (ver * 1e-3) / 1e9, 1),
+           "roofline": {"bound": "hbm", "kernel": "expert blocks of the step (router + "
+                        "expert block per layer, one graph)",
+                        "achieved": round(wbytes / (ver * 1e-3) / 1e9, 1),
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(wbytes / (ver * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                        "traffic": None,
+                        "bytes": "distinct routed experts x payload, summed over layers"}}
+    if not args.no_cpu:
+        x_step = xs[n_steps - 1].transpose(0, 1).contiguous()
+        out["cpu_baseline"] = cpu_baseline_batch(stack, x_step, args.cpu_layers)
+    return out
 
 
 def hbm_copy(args):
@@ -301,7 +339,7 @@ def hbm_copy(args):
            "warmup": args.warmup, "higher_is_better": True, "dtype": "u8",
            "data": "synthetic", "config": {"workload": "hbm-copy-1GiB"},
            "peak": HBM_PEAK_GBS, **res}
-    print(json.dumps(out), flush=True)
+    return out
 
 
 def stream(args):
@@ -378,7 +416,123 @@ def stream(args):
            "lookups": d, "bytes_copied_per_token": int(copied / n_tok),
            "lookahead_recall": round(st.recall(), 4), "h2d_GBs": round(h2d, 1),
            "build_s": round(t_build, 1)}
-    print(json.dumps(out), flush=True)
+    # the loop's binding resource is the host link: the bytes copied per
+    # second against the link's published rate (PCIe 5.0 x16, one direction)
+    link = copied / wall / 1e9
+    out["roofline"] = {"bound": "host link", "kernel": "slot fills (hipMemcpyAsync per "
+                       "record, pinned host -> HBM)", "achieved": round(link, 2),
+                       "peak": PCIE_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(link / PCIE_PEAK_GBS, 4), "traffic": None,
+                       "measured_h2d_GBs": round(h2d, 1)}
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(st, xs[args.warmup:], args.cpu_repeats)
+    st.close()
+    st.store.close()
+    return out
+
+
+def single_layer(args):
+    """One Qwen3-30B-A3B-shaped MoE layer at batch 1 (128 experts in a
+    256-slot pool at a seeded random placement, router softmax top-8 with
+    renormalised scores, one bf16 N(0, 1) token per call): 64 calls of the
+    layer on 64 different tokens (router kernel + the two decode kernels
+    each) captured as one HIP graph, replayed back to back.  Reports the
+    time per call and the HBM rate of its bytes (8 routed experts' payload +
+    the router rows)."""
+    import torch
+    from moe_stream_amd import geometry as G
+    from moe_stream_amd import ops, synth
+    from moe_stream_amd.pool import SlotPool
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    geom = G.QWEN3_30B_A3B
+    store = synth.make_store(geom, geom.n_experts, dev, synth.SEED_BASE + 600)
+    pool = SlotPool(geom, 256, dev, store=store)
+    perm = synth.slot_permutation(256, geom.n_experts, synth.SEED_BASE + 601)
+    pool.fill(np.arange(geom.n_experts), perm)
+    W, _ = synth.router_weights(geom, 1, dev, synth.SEED_BASE + 602)
+    table = torch.tensor(perm, dtype=torch.int32, device=dev)
+    n = 64
+    xs = synth.hidden_states(n, 1, geom.d_model, dev, synth.SEED_BASE + 603)[:, 0]
+    bufs = ops.RouteBuffers(1, geom.top_k, 0, dev)
+    ws_r = torch.zeros(_lib_fn("moe_route_workspace")(1, geom.n_experts), dtype=torch.uint8,
+                       device=dev)
+    g = geom.c_geom()
+    ws_f = torch.zeros(_lib_fn("moe_ffn_decode_workspace")(C.byref(g), 1, geom.top_k),
+                       dtype=torch.uint8, device=dev)
+    y = torch.empty((1, geom.d_model), dtype=torch.bfloat16, device=dev)
+
+    def calls():
+        for i in range(n):
+            x = xs[i:i + 1]
+            ops.route(x, W[0], None, geom.routing, geom.norm_topk_prob, geom.top_k,
+                      table=table, bufs=bufs, workspace=ws_r)
+            ops.ffn_decode(pool, bufs.slot_refs, bufs.scores, x, out=y, workspace=ws_f)
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        calls()
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        calls()
+    reps = args.steps * n
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(args.steps):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    ops.check_device_error()
+    us = a.elapsed_time(b) * 1e3 / reps
+    nbytes = geom.top_k * geom.payload_bytes + geom.n_experts * geom.d_model * 2
+    gbs = nbytes / (us * 1e-6) / 1e9
+    out = {"value": round(gbs, 1), "unit": "GB/s", "us_per_layer": round(us, 3),
+           "layers_per_s": round(1e6 / us, 1),
+           "config": {"workload": "qwen3-30b-a3b-moe-layer", "experts": 128, "d_model": 2048,
+                      "d_ff": 768, "top_k": 8, "pool_slots": 256, "tokens": 1,
+                      "launch": f"{n} layer calls (router + gate/up + down each) in one "
+                                f"HIP graph, {args.steps} replays"},
+           "roofline": {"bound": "hbm", "kernel": "route_kernel + ffn_gate_up_kernel + "
+                        "ffn_down_kernel (one layer)", "achieved": round(gbs, 1),
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                        "bytes_per_layer": nbytes}}
+    if not args.no_cpu:
+        import torch as _t
+        from oracle import cpu_block as CB
+        from oracle import layout as OL
+        threads = len(os.sched_getaffinity(0))
+        _t.set_num_threads(threads)
+        ex = {e: CB.Expert(OL.split_record(store[e].cpu().numpy(), geom.d_model, geom.d_ff,
+                                           False)) for e in range(geom.n_experts)}
+        Wc = W[0].float().cpu()
+        xh = xs.float().cpu()
+        ms = []
+        for i in range(args.cpu_repeats + 3):
+            t0 = time.perf_counter()
+            CB.moe_layer(xh[i % n], Wc, None, lambda e: ex[e], geom.top_k, geom.routing,
+                         geom.norm_topk_prob, "qwen3")
+            if i >= 3:
+                ms.append((time.perf_counter() - t0) * 1e3)
+        med = float(np.median(ms))
+        out["cpu_baseline"] = {"value": round(nbytes / (med * 1e-3) / 1e9, 3), "unit": "GB/s",
+                               "us_per_layer": round(med * 1e3, 1), "cores": threads,
+                               "kind": "port",
+                               "label": "CPU restatement (not MLX): torch on the host cores",
+                               "sample": f"{len(ms)} single-token layer calls (router + "
+                                         "top-8 + 8 experts), 3 warm-up; median"}
+    del pool, store
+    return out
+
+
+def _lib_fn(name):
+    from moe_stream_amd import _lib
+    return getattr(_lib.lib(), name)
 
 
 def time_dominant_kernel(stack, xs, n_tok):
@@ -422,6 +576,56 @@ def time_dominant_kernel(stack, xs, n_tok):
     return float(np.mean(ms)), float(np.median(ms)), len(ms)
 
 
+def _record(stack, idx):
+    """Store record idx as host bytes (a device store or a pinned host store)."""
+    arr = getattr(stack.store, "array", None)
+    return arr[idx] if arr is not None else stack.store[idx].cpu().numpy()
+
+
+def cpu_baseline_batch(stack, x_step, n_layers):
+    """The many-token expert path on the host cores: oracle.cpu_block's
+    moe_layer_batch (every token routed at once, each routed expert
+    dequantised once and applied to all its rows by one fp32 matrix product,
+    MLX's bf16 rounding points; not MLX), `n_layers` layer-blocks of the
+    stack spread over its layers, each timed on its own with the routed
+    experts read from the store before its timer starts.  tok/s = T tokens /
+    (n_layers_of_stack x median layer-block time)."""
+    import torch
+    from oracle import cpu_block as CB
+    from oracle import layout as OL
+    g = stack.geom
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    kind = "gptoss" if g.has_proj_bias else "qwen3"
+    T = x_step.shape[1]
+    layers = np.linspace(0, stack.L - 1, n_layers).round().astype(int).tolist()
+    ms = []
+    for i, Lx in enumerate([layers[0]] + layers):       # the first run is a warm-up
+        X = x_step[Lx].float().cpu()
+        W = stack.W[Lx].float().cpu()
+        b = None if stack.bias is None else stack.bias[Lx].float().cpu()
+        ids, _ = CB.route_rows(X, W, b, g.top_k, g.routing, g.norm_topk_prob)
+        ex = {int(e): CB.Expert(OL.split_record(_record(stack, Lx * stack.E + int(e)),
+                                                g.d_model, g.d_ff, g.has_proj_bias))
+              for e in torch.unique(ids).tolist()}
+        t0 = time.perf_counter()
+        CB.moe_layer_batch(X, W, b, lambda e: ex[e], g.top_k, g.routing,
+                           g.norm_topk_prob, kind, g.alpha, g.limit)
+        if i > 0:
+            ms.append((time.perf_counter() - t0) * 1e3)
+        del ex
+    ms = np.array(ms)
+    med = float(np.median(ms))
+    return {"value": round(T / (stack.L * med * 1e-3), 3), "unit": "tok/s", "cores": threads,
+            "kind": "port", "label": "CPU restatement (not MLX): torch on the host cores, "
+            "experts dequantised once per layer-block",
+            "layer_ms": {"median": round(med, 2), "min": round(float(ms.min()), 2),
+                         "max": round(float(ms.max()), 2)},
+            "sample": f"{len(ms)} layer-blocks of {T} tokens (router + top-{g.top_k} + the "
+                      f"routed experts) at layers {layers}, 1 warm-up; tok/s = {T} / "
+                      f"({stack.L} x median layer time)"}
+
+
 def cpu_baseline(stack, xs, repeats, gpu_token=None):
     """The expert path on the host cores: oracle.cpu_block, a torch CPU
     restatement of the reference graph (router + top-k + the k-expert block,
@@ -452,8 +656,8 @@ def cpu_baseline(stack, xs, repeats, gpu_token=None):
         if key not in cache:
             if len(cache) >= 64:
                 cache.pop(next(iter(cache)))
-            rec = stack.store[Lx * stack.E + e].cpu().numpy()
-            cache[key] = CB.Expert(OL.split_record(rec, g.d_model, g.d_ff, g.has_proj_bias))
+            cache[key] = CB.Expert(OL.split_record(_record(stack, Lx * stack.E + e),
+                                                   g.d_model, g.d_ff, g.has_proj_bias))
         return cache[key]
 
     cpu_ms, gpu_us = [], []
@@ -499,21 +703,9 @@ def cpu_baseline(stack, xs, repeats, gpu_token=None):
     return out
 
 
-def main():
-    args = parse()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build runs the expert path on one GPU "
-              "(a bs=1 decode stack is one independent replica per GPU); run with --gpus 1",
-              file=sys.stderr)
-        sys.exit(2)
-    if args.workload == "qwen3-prefill":
-        return prefill(args)
-    if args.workload == "qwen3-stream":
-        return stream(args)
-    if args.workload == "hbm-copy":
-        return hbm_copy(args)
-    if args.workload == "qwen3-verify":
-        return verify(args)
+def decode(args):
+    """The decode stacks (bs=1, one token at a time): the 48-layer Qwen3
+    stack (the headline) or the 36-layer gpt-oss stack."""
     import torch
     from moe_stream_amd import synth
     dev = torch.device("cuda:0")
@@ -642,9 +834,72 @@ def main():
             b.record(gs)
             b.synchronize()
             return a.elapsed_time(b) * 1e3
-        out["cpu_baseline"] = cpu_baseline(stack, xs, max(60, args.cpu_repeats), gpu_token)
+        out["cpu_baseline"] = cpu_baseline(stack, xs, args.cpu_repeats, gpu_token)
         if mode == "persistent":
             stack.check_persistent()
+    return out
+
+
+def _sub_args(args, **kw):
+    a = argparse.Namespace(**vars(args))
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+# the other benchmark configurations, measured after the headline in the
+# default run: (key, function, arguments); short step counts, bounded CPU samples
+SECONDARY = (
+    ("qwen3_layer", single_layer, dict(steps=4, warmup=1, cpu_repeats=60)),
+    ("gptoss_36l", decode, dict(workload="gptoss-36l", mode="auto", tokens=16, steps=2,
+                                warmup=1, cpu_repeats=24)),
+    ("qwen3_prefill_512", prefill, dict(workload="qwen3-prefill", tokens=512, steps=2,
+                                        warmup=1, cpu_layers=2)),
+    ("qwen3_verify_8", verify, dict(workload="qwen3-verify", tokens=8, steps=4, warmup=1,
+                                    verify_block="auto", cpu_layers=8)),
+    ("qwen3_stream_256", stream, dict(workload="qwen3-stream", tokens=256, warmup=2,
+                                      engine="native", pool_layout="records", depths="1",
+                                      cpu_repeats=48)),
+)
+
+
+def secondaries(args):
+    """Every other benchmark configuration, each with its roofline and a CPU
+    baseline of the same configuration; a failure is reported in its entry."""
+    import gc
+    import torch
+    res = {}
+    for key, fn, kw in SECONDARY:
+        t0 = time.perf_counter()
+        print(f"[bench] {key} ...", file=sys.stderr, flush=True)
+        try:
+            r = fn(_sub_args(args, **kw))
+        except Exception as e:          # report, keep the headline line
+            r = {"error": f"{type(e).__name__}: {e}"}
+        r["driver_s"] = round(time.perf_counter() - t0, 1)
+        res[key] = r
+        gc.collect()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return res
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build runs the expert path on one GPU "
+              "(a bs=1 decode stack is one independent replica per GPU); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+    fn = {"qwen3-prefill": prefill, "qwen3-stream": stream, "hbm-copy": hbm_copy,
+          "qwen3-verify": verify, "qwen3-layer": single_layer}.get(args.workload, decode)
+    out = fn(args)
+    if args.workload == "qwen3-48l" and not args.no_secondary:
+        import gc
+        import torch
+        gc.collect()
+        torch.cuda.empty_cache()
+        out["secondary"] = secondaries(args)
     print(json.dumps(out), flush=True)
 
 

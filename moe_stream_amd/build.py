@@ -28,7 +28,15 @@ HIPCC_FLAGS = [
     "-shared",
     # no packed fp32 instructions anywhere in device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # MFMA results straight into VGPRs (no accumulator-register copies)
+    # MFMA results straight into VGPRs (no accumulator-register copies).
+    # Under this flag the compiler can hand an MFMA's accumulator-input
+    # registers to a VALU result a few instructions after the MFMA issues,
+    # before the MFMA has read them (chained MFMAs whose destination differs
+    # from their accumulator input).  grouped.hip keeps each chain's first
+    # result alive with an empty asm use until the fold has read the chain's
+    # output; the ragged-tile cases of tests/test_gpu_grouped.py returned
+    # wrong outputs without it.  Changing this flag or the compiler calls for
+    # those tests and a scan of the built assembly for such a write.
     "-Xarch_device", "-mllvm=-amdgpu-mfma-vgpr-form=1",
     "-Wno-unused-command-line-argument",
 ]

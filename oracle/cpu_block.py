@@ -15,6 +15,10 @@ states it.  Each 4-bit product dequantises first (codes decoded through a
 256-entry byte table, w = S*q + B in fp32, kernels.py:104-106) and then
 runs one fp32 matrix-vector product; gate and up share one product.
 
+``moe_layer_batch`` is the many-token form (prefill, speculative
+verification): every token routed at once, each routed expert dequantised
+once and applied to all rows routed to it by one fp32 matrix product.
+
 Parity: pinned against ``numerics`` (fp64 and MLX-emulation) in
 tests/test_cpu_block.py at 2e-2 max relative error, routed ids as sets.
 """
@@ -63,6 +67,14 @@ class QuantMatrix:
         w = torch.index_select(_LUT, 0, self.codes).view(self.n_out, -1, GROUP)
         w.mul_(self.S).add_(self.B)
         return torch.mv(w.view(self.n_out, self.n_in), x)
+
+    def matmul(self, X: torch.Tensor) -> torch.Tensor:
+        """fp32 Y = X @ deq(W)^T for the rows X [n, n_in]: the matrix is
+        dequantised once for all rows (the batched gather_qmm of the prefill
+        path, engine_v3.py:588-600)."""
+        w = torch.index_select(_LUT, 0, self.codes).view(self.n_out, -1, GROUP)
+        w.mul_(self.S).add_(self.B)
+        return X @ w.view(self.n_out, self.n_in).t()
 
 
 class Expert:
@@ -127,4 +139,61 @@ def moe_layer(x: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None, exper
     for j in range(k):
         yj = _bf16(expert_ffn(x, experts(int(ids[j])), kind, alpha, limit) * sc[j])
         y = yj if y is None else y + yj
+    return ids, sc, _bf16(y)
+
+
+def _proj_rows(m: QuantMatrix, X: torch.Tensor) -> torch.Tensor:
+    Y = _bf16(m.matmul(X))
+    if m.bias is not None:
+        Y = _bf16(Y + m.bias)
+    return Y
+
+
+def expert_ffn_rows(X: torch.Tensor, e: Expert, kind: str, alpha: float, limit: float):
+    """expert_ffn for the rows X [n, D] routed to one expert."""
+    gu = _proj_rows(e.gate_up, X)
+    gate, up = gu[:, :e.d_ff], gu[:, e.d_ff:]
+    if kind == "qwen3":
+        h = _bf16(_bf16(gate * torch.sigmoid(gate)) * up)
+    else:
+        g = torch.clamp(gate, max=limit)
+        u = torch.clamp(up, -limit, limit)
+        h = _bf16(_bf16(g * torch.sigmoid(alpha * g)) * (u + 1.0))
+    return _proj_rows(e.down, h)
+
+
+def route_rows(X: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None, k: int,
+               routing: int, norm: bool):
+    """route() for the tokens X [T, D] at once; returns (ids, scores) [T, k]."""
+    Z = X @ W.t()
+    if bias is not None:
+        Z = Z + bias
+    Z = _bf16(Z)
+    if routing == 0:
+        P = _bf16(torch.softmax(Z, 1))
+        sc, ids = torch.topk(P, k, dim=1)
+        if norm:
+            sc = _bf16(sc / _bf16(sc.sum(1, keepdim=True)))
+    else:
+        zs, ids = torch.topk(Z, k, dim=1)
+        sc = _bf16(torch.softmax(zs, 1))
+    return ids, sc
+
+
+def moe_layer_batch(X: torch.Tensor, W: torch.Tensor, bias: torch.Tensor | None, experts,
+                    k: int, routing: int, norm: bool, kind: str, alpha: float = 1.702,
+                    limit: float = 7.0):
+    """T tokens X [T, D] through one layer: every token routed, each routed
+    expert run once over all its rows (`experts(e)` -> Expert), then per
+    token the score-weighted bf16 combine in rank order."""
+    ids, sc = route_rows(X, W, bias, k, routing, norm)
+    T = X.shape[0]
+    Y = torch.zeros((T, k, W.shape[1]), dtype=torch.float32)
+    for e in torch.unique(ids).tolist():
+        t, r = torch.nonzero(ids == e, as_tuple=True)
+        Y[t, r] = expert_ffn_rows(X[t], experts(int(e)), kind, alpha, limit)
+    P = _bf16(Y * sc.unsqueeze(-1))
+    y = P[:, 0]
+    for j in range(1, k):
+        y = y + P[:, j]
     return ids, sc, _bf16(y)

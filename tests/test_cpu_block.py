@@ -76,3 +76,35 @@ def test_quant_matrix_is_dequant_then_dot():
     ref = np.concatenate([N.dequant(w1, s1, b1) @ x, N.dequant(w2, s2, b2) @ x])
     assert np.allclose(y, ref, rtol=1e-5, atol=1e-5)
     assert np.allclose(y[3:], 7.0 * x.astype(np.float64).sum(), rtol=1e-5)
+
+
+@pytest.mark.parametrize("kind,D,F,E,k,routing,norm", [
+    ("qwen3", 256, 128, 16, 4, 0, True),
+    ("gptoss", 192, 192, 16, 4, 1, False),
+])
+def test_cpu_layer_batch_matches_oracle_and_per_token(kind, D, F, E, k, routing, norm):
+    """The many-token form: routed ids equal the per-token form's token by
+    token, outputs within the FFN tolerance of the batched oracle (both
+    modes)."""
+    rng = np.random.default_rng(20260702)
+    bias = kind == "gptoss"
+    recs = [_record(rng, D, F, bias) for _ in range(E)]
+    experts = [CB.Expert(r) for r in recs]
+    Wb = N.f32_to_bf16_bits(rng.normal(0, 0.02, (E, D)))
+    bb = N.f32_to_bf16_bits(rng.normal(0, 0.02, E)) if bias else None
+    W = CB._bits_to_f32(Wb)
+    bt = None if bb is None else CB._bits_to_f32(bb)
+    T = 24
+    xb = N.f32_to_bf16_bits(rng.normal(0, 1, (T, D)))
+    X = CB._bits_to_f32(xb)
+    ids, sc, Y = CB.moe_layer_batch(X, W, bt, lambda e: experts[e], k, routing, norm, kind)
+    for t in range(T):
+        i1, s1, y1 = CB.moe_layer(X[t], W, bt, lambda e: experts[e], k, routing, norm, kind)
+        assert set(i1.tolist()) == set(ids[t].tolist()), t
+        assert N.rel_err(Y[t].double().numpy(), y1.double().numpy()) < 1e-2, t
+    X64 = N.bf16_bits_to_f32(xb).astype(np.float64)
+    for mode in ("f64", "mlx"):
+        ref = N.moe_block_batch(X64, ids.numpy(), sc.double().numpy(), lambda e: recs[e],
+                                kind, mode)
+        err = max(N.rel_err(Y[t].double().numpy(), ref[t]) for t in range(T))
+        assert err < TOL, (kind, mode, err)
