@@ -119,6 +119,15 @@ constexpr int kCounterWords = kSub * 32;
 // K + kSpare - 1): a routed expert among them needs no fix-up pass.
 constexpr int kSpare = 2;
 
+// Widest layer output the per-rank partial outputs of the workspace hold.
+constexpr int kStackMaxD = 2880;
+
+// Workgroup w runs on XCD w % kXcds (the dispatcher deals workgroups to the
+// XCDs round robin), so the workgroups with one value of w % kXcds share
+// an L2: a plain store there is seen by an agent-scope load from any of
+// them, without the round trip through the device-coherent path.
+constexpr int kXcds = 8;
+
 // Counters of one layer: the layer output (the layer boundary).  Router
 // logits and expert activations carry their own flags instead.
 enum { CNT_D = 0 };
@@ -147,7 +156,8 @@ __device__ __forceinline__ void put_logit(uint64_t *slot, float v, uint32_t fl) 
 //   abort word (256 B) | router + lookahead logits [2][kRouteMaxE], flagged
 //   8-byte entries | activations of the predicted and spare experts
 //   [K + kSpare][F/2] and of the fix-up slots [K][F/2] (2 bf16 + layer flag
-//   per 8 bytes) | counters [L][kSub], 128 B apart
+//   per 8 bytes) | score-weighted down outputs per routing rank, fp32
+//   [2 (layer parity)][K][kStackMaxD] | counters [L][kSub], 128 B apart
 template <int F, int K>
 struct StackWs {
   static constexpr size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -155,7 +165,8 @@ struct StackWs {
   static constexpr size_t kLgt = 256;
   static constexpr size_t kHpred = kLgt + al((size_t)2 * kRouteMaxE * 8);
   static constexpr size_t kHfix = kHpred + al((size_t)(K + kSpare) * (F / 2) * 8);
-  static constexpr size_t kCnt = kHfix + al((size_t)K * (F / 2) * 8);
+  static constexpr size_t kPart = kHfix + al((size_t)K * (F / 2) * 8);
+  static constexpr size_t kCnt = kPart + al((size_t)2 * K * kStackMaxD * 4);
   static constexpr size_t bytes(int L) {
     return kCnt + (size_t)L * kCountersPerLayer * kCounterWords * 4;
   }
@@ -312,6 +323,21 @@ __device__ __forceinline__ void put_acts(uint64_t *hf, uint32_t hb, uint32_t fl)
                        __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(hf + 1, (uint64_t)(h2 | (h3 << 16)) | f, __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// put_acts for readers on this workgroup's XCD only: plain 8-byte stores,
+// which stay in the XCD's L2 (agent-scope loads on the same XCD see them;
+// workgroups on other XCDs must not read these entries).
+__device__ __forceinline__ void put_acts_xcd(uint64_t *hf, uint32_t hb, uint32_t fl) {
+  const uint32_t h0 = __builtin_amdgcn_readlane(hb, 0), h1 = __builtin_amdgcn_readlane(hb, 16);
+  const uint32_t h2 = __builtin_amdgcn_readlane(hb, 32), h3 = __builtin_amdgcn_readlane(hb, 48);
+  if ((threadIdx.x & 63) == 0) {
+    const uint64_t f = (uint64_t)fl << 32;
+    __hip_atomic_store(hf, (uint64_t)(h0 | (h1 << 16)) | f, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_store(hf + 1, (uint64_t)(h2 | (h3 << 16)) | f, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 }
 
@@ -579,6 +605,34 @@ __device__ __forceinline__ void get_acts(const uint64_t *hf, uint32_t fl, const 
   }
 }
 
+// One whole wave: pieces [PPW * w, PPW * w + PPW) of one expert's F
+// activations (16-byte pieces of 8 bf16, 4 flagged entries each; lane j <
+// PPW takes piece PPW * w + j), polled until each carries the flag `fl`.
+// Lanes past PPW load the wave's first piece and do not wait on it.
+template <int PPW>
+__device__ __forceinline__ uint4 get_acts_part(const uint64_t *hf, int w, uint32_t fl,
+                                               const Abort &ab) {
+  const int lane = threadIdx.x & 63;
+  const bool mine = lane < PPW;
+  const uint64_t *e = hf + 4 * (PPW * w + (mine ? lane : 0));
+  uint32_t spins = 0;
+  uint4 p;
+  while (true) {
+    uint64_t v[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      v[q] = __hip_atomic_load(e + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bool ok = true;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) ok = ok && (uint32_t)(v[q] >> 32) == fl;
+    p = make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+    if (__ballot(mine && !ok) == 0) break;
+    if (ab.gave_up(++spins)) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return p;
+}
+
 // Register loads of one workgroup's gate/up block (waves 0..WAVES_U-1: the
 // codes of its rows; every thread: its share of the block's scales).
 template <class C>
@@ -663,12 +717,23 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
   constexpr int FT = F / 4;          // 4-row tasks per expert (fix-up, spares)
   constexpr int NWG = C::ITEMS_D;    // the grid
   static_assert(K * FT <= C::WAVES_U * NWG && kSpare <= K, "every task has a wave");
+  // expert position p (gate/up and down rows) on the workgroups w with
+  // w % K == p, i.e. on one XCD, so its activations stay in that XCD's L2
+  constexpr int WPP = NWG / K;       // workgroups per position
+  constexpr int DROWS_WG = D / WPP;  // a workgroup's down rows of its position
+  static_assert(K == kXcds && NWG == K * NPOS && DROWS_WG == 8 * ROWS_D,
+                "one position per XCD; 8 waves of ROWS_D down rows per workgroup");
+  constexpr int PPW = HU4 / 8;       // activation pieces each wave polls
+  static_assert(HU4 % 8 == 0 && PPW % 4 == 0 && PPW <= 64, "activation pieces per wave");
+  static_assert(K * ROWS_D == 64 && D <= kStackMaxD, "the combine: one lane per (rank, row)");
+  constexpr int W_COMB = C::WAVES_U - 1;   // the wave that combines the previous layer
 
   __shared__ uint4 act_l[4 * U];
   __shared__ float asum_l[U];
   __shared__ uint4 sbu_l[4][SB_U4];
-  __shared__ uint4 hact_l[K][4 * UF];
-  __shared__ float hsum_l[K][UF];
+  __shared__ uint4 hact_l[K][4 * UF];   // per wave: fix-up tasks' scale scratch
+  __shared__ uint4 hact_s[4 * UF];      // the position's activations (down input)
+  __shared__ float hsum_s[UF];
   __shared__ uint4 sbd_l[K][2 * SBD_U4];
   __shared__ float red_l[K][ROWS_D];
   __shared__ int sel_id[K];
@@ -693,8 +758,10 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
   uint64_t *const lgt = reinterpret_cast<uint64_t *>(a.ws + WS::kLgt);
   uint64_t *const hpred = reinterpret_cast<uint64_t *>(a.ws + WS::kHpred);
   uint64_t *const hfix = reinterpret_cast<uint64_t *>(a.ws + WS::kHfix);
-  const int upos = wg / NPOS, urow0 = (wg % NPOS) * ROWS_U;   // gate/up block
-  const int drow0 = wg * ROWS_D;                               // down block
+  float *const part = reinterpret_cast<float *>(a.ws + WS::kPart);
+  const int upos = wg % K, urow0 = (wg / K) * ROWS_U;          // gate/up block
+  const int dwrow = (wg / K) * DROWS_WG + wave * ROWS_D;       // this wave's down rows
+  const int drow0 = wg * ROWS_D;                               // combined output rows
   const int dj = lane % SGD, dsub = lane / SGD;
   if (tid < 2) {
     pred_cnt[tid] = 0;               // layer 0 has no prediction
@@ -742,8 +809,9 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
     if (wave == 0) trace_mark(a, l, TR_R_WAITED);
     const int pcnt = pred_cnt[l & 1];
     const int *P = pred_buf[l & 1];
-    if (wave == W_RANK && W_RANK < pcnt) d_load<C>(a, pred_ref[l & 1][W_RANK], drow0, cd, sdr);
+    if (wave == W_RANK && upos < pcnt) d_load<C>(a, pred_ref[l & 1][upos], dwrow, cd, sdr);
     // ------------------------------------------------------- role split ----
+    uint32_t comb = 0;   // wave W_COMB: one partial output of layer l-1 per lane
     if (wave < W_ROUTER) {
       // stage x_l (pair order + 32-input sums) and the predicted block's
       // scales; the six gate/up waves then meet on an LDS counter, so the
@@ -789,10 +857,17 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       uint32_t hs = 0;
       if (spare) hs = task_rows_lds<C>(a, sref, sok, ts % FT, spare_l[wave], act_l, asum_l);
       if (urows)
-        put_acts(hpred + (size_t)upos * (F / 2) + (urow0 + wave * C::RPSU) / 2, hu,
-                 layer_flag(a, l));
+        put_acts_xcd(hpred + (size_t)upos * (F / 2) + (urow0 + wave * C::RPSU) / 2, hu,
+                     layer_flag(a, l));
       if (spare)
         put_acts(hpred + (size_t)(K + ts / FT) * (F / 2) + 2 * (ts % FT), hs, layer_flag(a, l));
+      // layer l-1's score-weighted outputs of this workgroup's rows, complete
+      // since this layer's start: loaded now, summed before the arrival
+      if (wave == W_COMB && l > 0)
+        comb = __hip_atomic_load(reinterpret_cast<const uint32_t *>(
+                                     part + ((size_t)((l - 1) & 1) * K + lane / ROWS_D) *
+                                                kStackMaxD + drow0 + lane % ROWS_D),
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (wave == 0) trace_mark(a, l, TR_U_ARRIVED);
     } else if (wave == W_ROUTER) {
       // one router row (the lane partition and summation order of
@@ -977,16 +1052,11 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       KARG(refs_out)[(size_t)l * K + tid] = sel_ref[tid];
       if (sel_ref[tid] < 0) atomicAdd(KARG(miss) + l, 1);
     }
-    // down rows of a routed expert that was not predicted: loaded now, so
-    // their latency overlaps the fix-up pass
-    int d_r = 0, d_fx = -1;
-    int32_t d_ref = 0;
-    if (wave < K) {
-      d_r = d_rank[wave];
-      d_fx = d_fix[wave];
-      d_ref = sel_ref[d_r];
-      if (d_fx >= 0) d_load<C>(a, d_ref, drow0, cd, sdr);
-    }
+    // this position's routed expert; its down rows, if it was not the
+    // predicted one, loaded now so their latency overlaps the fix-up pass
+    const int d_r = d_rank[upos], d_fx = d_fix[upos];
+    const int32_t d_ref = sel_ref[d_r];
+    if (d_fx >= 0) d_load<C>(a, d_ref, dwrow, cd, sdr);
     // ------------------------------------------ fix-up: unpredicted ----
     // Spread over the whole grid: task t = wave * (grid) + workgroup of the
     // gate/up waves computes 4 rows of fix-up slot t / FT, so one miss costs
@@ -999,13 +1069,15 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       if (wave == 0) trace_mark(a, l, TR_FIXED);
     }
     // ------------------------------------------------------------ D_l ----
-    if (wave < K) {
+    // The position's routed expert, ROWS_D rows per wave: each wave polls
+    // PPW pieces of its activations (XCD-local entries for the predicted
+    // expert) into the shared LDS copy, then its rows' score-weighted outputs
+    // go to the rank's partial output row (summed in rank order by the
+    // combine, after the layer).
+    {
       const int r = d_r, fx = d_fx;
       const int32_t dref = d_ref;
       const char *dw = resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_W, NP), dref);
-
-      uint4 *hact = hact_l[wave];
-      float *hsum = hsum_l[wave];
       if (dw != nullptr) {
         uint4 *sbd = sbd_l[wave];
 #pragma unroll
@@ -1013,32 +1085,22 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
           const int i = it * 64 + lane;
           if (i < 2 * SBD_U4) sbd[i] = sdr[it];
         }
-        // the expert's F activations: 8 bf16 per 16-byte piece, <= 2 per lane
-        static_assert(HU4 <= 128, "two pieces per lane");
-        const int i0 = lane, i1 = lane + 64;
-        uint4 p0, p1;
         const int src = fx < 0 ? 0 : miss_src[fx];
-        const uint64_t *hf = fx < 0    ? hpred + (size_t)wave * (F / 2)
+        const uint64_t *hf = fx < 0    ? hpred + (size_t)upos * (F / 2)
                              : src >= 0 ? hfix + (size_t)src * (F / 2)
                                         : hpred + (size_t)(K - 1 - src) * (F / 2);
-        get_acts<HU4>(hf, layer_flag(a, l), ab, p0, p1);
+        const uint4 pc = get_acts_part<PPW>(hf, wave, layer_flag(a, l), ab);
         if (wave == 0) trace_mark(a, l, TR_D_WAITED);
-#pragma unroll
-        for (int it = 0; it < 2; ++it) {
-          const int i = it ? i1 : i0;
-          float s = 0.f;
-          if (i < HU4) s = stage_piece<UF>(hact, i, it ? p1 : p0);
-          s += dpp_f<kDppQuadXor1>(s);
-          s += dpp_f<kDppQuadXor2>(s);
-          if (i < HU4 && (i & 3) == 0) hsum[i >> 2] = s;
-        }
-      } else if (lane == 0) {
+        const int i = PPW * wave + lane;
+        float s = 0.f;
+        if (lane < PPW) s = stage_piece<UF>(hact_s, i, pc);
+        s += dpp_f<kDppQuadXor1>(s);
+        s += dpp_f<kDppQuadXor2>(s);
+        if (lane < PPW && (i & 3) == 0) hsum_s[i >> 2] = s;
+      } else if (wave == 0 && lane == 0) {
         flag_error();
       }
-      // same-wave LDS handoff: staging above, reads below
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
-      __builtin_amdgcn_wave_barrier();
-      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __syncthreads();   // every wave's pieces staged
       float p = 0.f;
       if (dw != nullptr) {
         const uint16_t *sbh = reinterpret_cast<const uint16_t *>(sbd_l[wave]);
@@ -1049,7 +1111,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
           if (CPLD * SGD == UF || c < UF) {
             const int g = dsub * NGF + (c >> 1);
             const float Sd = bf16_to_f32(sbh[g]), Bd = bf16_to_f32(sbh[SBN + g]);
-            p += Sd * chunk_dot_lds<UF>(cd[i], hact_l[wave], c) + (Bd - 128.f * Sd) * hsum_l[wave][c];
+            p += Sd * chunk_dot_lds<UF>(cd[i], hact_s, c) + (Bd - 128.f * Sd) * hsum_s[c];
           }
         }
       }
@@ -1057,15 +1119,25 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       if (dj == 0) {
         if (PBIAS && dw != nullptr)
           p += bf16_to_f32(reinterpret_cast<const uint16_t *>(
-              resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_BIAS, NP), dref))[drow0 + dsub]);
-        red_l[r][dsub] = (dw != nullptr) ? sel_sc[r] * p : 0.f;
+              resolve_packed<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_BIAS, NP), dref))[dwrow + dsub]);
+        const float v = (dw != nullptr) ? sel_sc[r] * p : 0.f;
+        __hip_atomic_store(reinterpret_cast<uint32_t *>(
+                               part + ((size_t)(l & 1) * K + r) * kStackMaxD + dwrow + dsub),
+                           __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    __syncthreads();
-    if (tid < ROWS_D) {
-      float yv = 0.f;
-      for (int w = 0; w < K; ++w) yv += red_l[w][tid];   // rank order
-      KARG(y)[(size_t)l * D + drow0 + tid] = (uint16_t)f32_to_bf16(yv);
+    // the combine of layer l-1 (its partials were loaded during this layer):
+    // ROWS_D output rows, the k ranks summed in rank order
+    if (wave == W_COMB && l > 0) {
+      red_l[lane / ROWS_D][lane % ROWS_D] = __uint_as_float(comb);
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      __builtin_amdgcn_wave_barrier();
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+      if (lane < ROWS_D) {
+        float yv = 0.f;
+        for (int w = 0; w < K; ++w) yv += red_l[w][lane];   // rank order
+        KARG(y)[(size_t)(l - 1) * D + drow0 + lane] = (uint16_t)f32_to_bf16(yv);
+      }
     }
     wg_arrive(counter<WS>(a, l, CNT_D));
     if (wave == 0) trace_mark(a, l, TR_D_ARRIVED);
@@ -1075,7 +1147,25 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       const int pc = pred_cnt[(l + 1) & 1];
       const int32_t *Rn = pred_ref[(l + 1) & 1];
       if (upos < pc) u_load<C>(a, Rn[upos], urow0, cg, cu, sr);
-      if (wave < K && wave != W_RANK && wave < pc) d_load<C>(a, Rn[wave], drow0, cd, sdr);
+      if (wave != W_RANK && upos < pc) d_load<C>(a, Rn[upos], dwrow, cd, sdr);
+    }
+  }
+  // the last layer's outputs: its partials are complete once every
+  // workgroup has arrived
+  wg_wait(counter<WS>(a, a.L - 1, CNT_D), ep * C::ITEMS_D, W_RANK, ab);
+  if (wave == W_COMB) {
+    const float v = __uint_as_float(__hip_atomic_load(
+        reinterpret_cast<const uint32_t *>(part + ((size_t)((a.L - 1) & 1) * K + lane / ROWS_D) *
+                                                      kStackMaxD + drow0 + lane % ROWS_D),
+        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    red_l[lane / ROWS_D][lane % ROWS_D] = v;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_wave_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (lane < ROWS_D) {
+      float yv = 0.f;
+      for (int w = 0; w < K; ++w) yv += red_l[w][lane];   // rank order
+      KARG(y)[(size_t)(a.L - 1) * D + drow0 + lane] = (uint16_t)f32_to_bf16(yv);
     }
   }
 }
