@@ -87,9 +87,10 @@ __device__ __forceinline__ T karg_load(size_t off) {
 // Phase trace: wall-clock stamps of thread 0 of the first kTraceWGs
 // workgroups at each phase boundary of each layer.
 constexpr int kTraceWGs = 256;
-constexpr int kTracePoints = 12;
+constexpr int kTracePoints = 15;
 enum { TR_START, TR_R_WAITED, TR_R_ARRIVED, TR_SELECTED, TR_U_ARRIVED,
-       TR_D_WAITED, TR_D_ARRIVED, TR_R_ALL, TR_LOGITS, TR_SOFTMAX, TR_TOPK, TR_FIXED };
+       TR_D_WAITED, TR_D_ARRIVED, TR_R_ALL, TR_LOGITS, TR_SOFTMAX, TR_TOPK, TR_FIXED,
+       TR_LOOKED, TR_SPARE1, TR_UROWS2 };
 
 // Called by one wave at a time; its lane 0 stamps.
 __device__ __forceinline__ void trace_mark(const StackArgs &a, int l, int point) {
@@ -869,6 +870,8 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
                                                 kStackMaxD + drow0 + lane % ROWS_D),
                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (wave == 0) trace_mark(a, l, TR_U_ARRIVED);
+      if (wave == 1) trace_mark(a, l, TR_SPARE1);
+      if (wave == 2) trace_mark(a, l, TR_UROWS2);
     } else if (wave == W_ROUTER) {
       // one router row (the lane partition and summation order of
       // route_kernel, so both paths produce bit-identical logits)
@@ -893,6 +896,9 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
         if (lane == 0) put_logit(lgt + (rnxt ? a.E : 0) + e, acc, layer_flag(a, l));
         trace_mark(a, l, TR_R_ARRIVED);
       }
+      // this wave's down rows, loaded once its router row is out (its x
+      // loads then have no staging loads ahead of them)
+      if (upos < pcnt) d_load<C>(a, pred_ref[l & 1][upos], dwrow, cd, sdr);
       // lookahead ranking of layer l+1: raw bf16 logits of its router on x_l
       if (has_next) {
         const int e0 = lane, e1 = lane + 64;
@@ -933,6 +939,7 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
           spare_cnt[(l + 1) & 1] = min(kSpare, max(0, ksel - K));   // a wider k_pred: ranks
                                                                      // past K + kSpare unused
         }
+        trace_mark(a, l, TR_LOOKED);
       }
     } else {
       // ---- routing: every workgroup ranks this layer's logits ----------
@@ -1142,12 +1149,13 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
     wg_arrive(counter<WS>(a, l, CNT_D));
     if (wave == 0) trace_mark(a, l, TR_D_ARRIVED);
     // ----------------------------- staging loads of layer l+1's prediction
-    // (the ranking wave's down rows are staged after the next layer's wait)
+    // (the ranking wave's down rows are staged after the next layer's wait,
+    // the router wave's after its router row)
     if (has_next) {
       const int pc = pred_cnt[(l + 1) & 1];
       const int32_t *Rn = pred_ref[(l + 1) & 1];
       if (upos < pc) u_load<C>(a, Rn[upos], urow0, cg, cu, sr);
-      if (wave != W_RANK && upos < pc) d_load<C>(a, Rn[upos], dwrow, cd, sdr);
+      if (wave != W_RANK && wave != W_ROUTER && upos < pc) d_load<C>(a, Rn[upos], dwrow, cd, sdr);
     }
   }
   // the last layer's outputs: its partials are complete once every
