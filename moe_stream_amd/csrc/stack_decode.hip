@@ -157,8 +157,9 @@ __device__ __forceinline__ void put_logit(uint64_t *slot, float v, uint32_t fl) 
 //   abort word (256 B) | router + lookahead logits [2][kRouteMaxE], flagged
 //   8-byte entries | activations of the predicted and spare experts
 //   [K + kSpare][F/2] and of the fix-up slots [K][F/2] (2 bf16 + layer flag
-//   per 8 bytes) | score-weighted down outputs per routing rank, fp32
-//   [2 (layer parity)][K][kStackMaxD] | counters [L][kSub], 128 B apart
+//   per 8 bytes) | score-weighted down outputs per routing rank, 8 bytes
+//   per entry (fp32, or fp32 + layer flag) [2 (layer parity)][K][kStackMaxD]
+//   | counters [L][kSub], 128 B apart
 template <int F, int K>
 struct StackWs {
   static constexpr size_t al(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -167,7 +168,7 @@ struct StackWs {
   static constexpr size_t kHpred = kLgt + al((size_t)2 * kRouteMaxE * 8);
   static constexpr size_t kHfix = kHpred + al((size_t)(K + kSpare) * (F / 2) * 8);
   static constexpr size_t kPart = kHfix + al((size_t)K * (F / 2) * 8);
-  static constexpr size_t kCnt = kPart + al((size_t)2 * K * kStackMaxD * 4);
+  static constexpr size_t kCnt = kPart + al((size_t)2 * K * kStackMaxD * 8);
   static constexpr size_t bytes(int L) {
     return kCnt + (size_t)L * kCountersPerLayer * kCounterWords * 4;
   }

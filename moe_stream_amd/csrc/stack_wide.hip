@@ -10,12 +10,13 @@
 // chain of dependent steps runs:
 //
 //   gate/up  240 workgroups x 48 rows of the expert PREDICTED at the
-//            workgroup's position (60 workgroups per position), held in
-//            the registers of waves 0-3 (one per SIMD, 12 rows each); the
+//            workgroup's position w % K (60 workgroups per position), held
+//            in the registers of waves 0-3 (one per SIMD, 12 rows each); the
 //            next layer's are loaded as soon as this layer's gate/up is done
-//   down     180 workgroups x 16 output rows of all K positions, staged in
-//            LDS (108 KiB of codes and scales) by direct-to-LDS loads of
-//            waves 4 and 5 at the layer start, beside the gate/up pass
+//   down     180 workgroups x 64 output rows of the expert at their position
+//            w % K (45 workgroups per position, 16 rows per down wave),
+//            staged in LDS (108 KiB of codes and scales) by direct-to-LDS
+//            loads of waves 4-7 once the routing is known
 //   router   wave 6: one router row (+ the lookahead row), then the
 //            lookahead ranking of layer l+1
 //   routing  wave 7: the layer boundary, x staged in LDS, the ranking of
@@ -23,16 +24,20 @@
 //   fix-up   a routed expert that was not predicted takes the position of a
 //            predicted expert that was not routed: that position's gate/up
 //            rows and down rows are loaded once the routing is known
-//   D        waves 6 and 7 collect the K experts' activations into LDS (they
-//            have no loads in flight, so their polls return at once); waves
-//            4-7 run the down rows of one position each (each SIMD pairs one
-//            of them with a gate/up wave); wave 7 combines in rank order,
-//            stores and arrives
+//   D        the four gate/up waves collect a quarter each of the
+//            activations of the workgroup's position into LDS (they have no
+//            loads in flight, so their polls return at once); waves 4-7 run
+//            16 down rows each and publish the score-weighted rows as
+//            flagged per-rank entries; wave 7 arrives
+//   combine  wave 5 of the next layer (idle until the routing) sums the
+//            previous layer's per-rank rows in rank order and stores them
+//            (the last layer's after the kernel's final boundary)
 //
 // Every row is summed over the lanes and in the order of ffn_decode's
 // gpt-oss instantiation (gate/up: 32 lanes per row; down: 16 lanes per row)
 // and the combine runs in rank order, so the outputs are bit-identical to
-// route_kernel + ffn_decode per layer.
+// route_kernel + ffn_decode per layer.  Each workgroup polls the activations
+// of one expert (11.5 KB), not of all K.
 //
 // Semantics per layer: top_k_route (engine_120b.py:65-70), top_k_indices
 // (engine_120b.py:73-75), the gpt-oss expert block with projection biases
@@ -58,16 +63,21 @@ struct WideCfg {
   // down: 16 lanes per row, 4 rows per unit, 4 units per position
   static constexpr int UF = F / 32, NGF = F / 64;
   static constexpr int SGD = 16, CPLD = (UF + SGD - 1) / SGD, RPSD = 64 / SGD;
-  static constexpr int RSTEPS_D = 4, ROWS_D = RSTEPS_D * RPSD;
-  static constexpr int ITEMS_D = D / ROWS_D;
+  static constexpr int RSTEPS_D = 4, ROWS_D = RSTEPS_D * RPSD;   // rows per down wave
+  static constexpr int WAVES_D = 4, ROWS_DWG = WAVES_D * ROWS_D;   // rows per workgroup
+  static constexpr int ITEMS_D = K * (D / ROWS_DWG);               // down workgroups
+  static constexpr int CROWS = D / ITEMS_D;                         // combined rows per workgroup
   static constexpr int SBD_U4 = ROWS_D * NGF * 2 / 16;
   static constexpr int DCI = RSTEPS_D * CPLD;          // code loads per position (1 KiB each)
   static constexpr int DSI = (2 * SBD_U4 + 63) / 64;   // scale loads per position
   static constexpr int NP = PBIAS ? 4 : 3;
   static constexpr int XU4 = D / 8, HU4 = F / 8;
   static constexpr int HPL = (HU4 + 63) / 64;          // activation pieces per lane
+  static constexpr int HPW = (HU4 / WAVES_U + 3) / 4 * 4;   // ... per gate/up wave (whole chunks)
+  static constexpr int HPWL = (HPW + 63) / 64;              // ... per lane of it
   static constexpr int XPL = (XU4 + 63) / 64;          // x pieces per lane (one wave)
-  static_assert(F % ROWS_U == 0 && D % ROWS_D == 0, "row blocks");
+  static_assert(F % ROWS_U == 0 && D % ROWS_DWG == 0 && D % ITEMS_D == 0, "row blocks");
+  static_assert(K * CROWS <= 64 && WAVES_U * HPW >= HU4, "combine lanes, activation quarters");
   static_assert(ITEMS_U <= NWG && ITEMS_D <= NWG, "one item per workgroup");
   static_assert((ROWS_U * NG * 2) % 16 == 0 && (ROWS_D * NGF * 2) % 16 == 0, "scale pieces");
   static_assert(K == 4 && WAVES_U == 4 && NT / 64 == 8,
@@ -168,6 +178,72 @@ __device__ __forceinline__ void get_acts_multi(int tid, const uint64_t *const (&
     if (__ballot(!ok) == 0) break;
     if (ab.gave_up(++spins)) break;
     __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// One whole wave: pieces [HPW * w, HPW * w + HPW) of one expert's F
+// activations (its F/2 flagged entries at hf; lane i takes pieces
+// HPW * w + i + 64 j, j < HPWL), polled until every one of them carries `fl`.
+// Lanes past the quarter re-read a clamped piece and do not wait on it; a
+// piece that arrived is not read again.  Bounded.
+template <int HU4, int HPW, int HPWL>
+__device__ __forceinline__ void get_acts_quarter(int tid, const uint64_t *hf, int w, uint32_t fl,
+                                                 const Abort &ab, uint4 (&p)[HPWL]) {
+  const int lane = tid & 63;
+  uint32_t spins = 0;
+  uint32_t got = 0;   // bit j: piece j of this lane complete (or not this lane's)
+#pragma unroll
+  for (int j = 0; j < HPWL; ++j) {
+    const int k = lane + 64 * j;
+    if (k >= HPW || HPW * w + k >= HU4) got |= 1u << j;
+  }
+  while (true) {
+#pragma unroll
+    for (int j = 0; j < HPWL; ++j) {
+      if ((got >> j) & 1u) continue;
+      const uint64_t *e = hf + 4 * min(HPW * w + lane + 64 * j, HU4 - 1);
+      uint64_t v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        v[q] = __hip_atomic_load(e + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      bool ok = true;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ok = ok && (uint32_t)(v[q] >> 32) == fl;
+      p[j] = make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+      got |= (uint32_t)ok << j;
+    }
+    if (__ballot(got != (1u << HPWL) - 1u) == 0) break;
+    if (ab.gave_up(++spins)) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// One whole wave (lane = rank * CROWS + row): the layer's combined output
+// rows [crow0, crow0 + CROWS) from the K per-rank flagged entries of `part`
+// (polled until each carries `fl`), summed in rank order through `red`.
+template <int K, int CROWS>
+__device__ __forceinline__ void wide_combine(const uint64_t *part, int crow0, uint32_t fl,
+                                             const Abort &ab, float (*red)[CROWS],
+                                             uint16_t *y) {
+  const int lane = threadIdx.x & 63;
+  const int r = min(lane / CROWS, K - 1), i = lane % CROWS;
+  const bool mine = lane < K * CROWS;
+  const uint64_t *e = part + (size_t)r * kStackMaxD + crow0 + i;
+  uint64_t v = __hip_atomic_load(e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t spins = 0;
+  while (__ballot(mine && (uint32_t)(v >> 32) != fl) != 0) {
+    if (ab.gave_up(++spins)) break;
+    __builtin_amdgcn_s_sleep(1);
+    v = __hip_atomic_load(e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (mine) red[r][i] = __uint_as_float((uint32_t)v);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_wave_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  if (lane < CROWS) {
+    float yv = 0.f;
+    for (int w = 0; w < K; ++w) yv += red[w][lane];   // rank order
+    y[crow0 + lane] = (uint16_t)f32_to_bf16(yv);
   }
 }
 
@@ -433,12 +509,13 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
   __shared__ float asum_l[U];
   __shared__ uint4 sbu_l[C::SUI_ALL * 64];    // gate/up scales (gate S | gate B | up S | up B)
   __shared__ uint32_t ubias_l[64];            // gate/up projection biases (bf16 pairs)
-  __shared__ uint4 dcode_l[K][C::DCI][64];    // down codes of each position
-  __shared__ uint4 dsc_l[K][C::DSI][64];      // their scales (S | B)
-  __shared__ uint4 hact_l[K][4 * UF];
-  __shared__ float hsum_l[K][UF];
-  __shared__ float dbias_l[K][ROWS_D];
-  __shared__ float red_l[K][ROWS_D];
+  __shared__ uint4 dcode_l[C::WAVES_D][C::DCI][64];   // down codes of each down wave's rows
+  __shared__ uint4 dsc_l[C::WAVES_D][C::DSI][64];     // their scales (S | B)
+  __shared__ uint4 hact_l[4 * UF];                    // the position's activations
+  __shared__ float hsum_l[UF];
+  __shared__ float dbias_l[C::WAVES_D][ROWS_D];
+  __shared__ float dred_l[C::WAVES_D][ROWS_D];        // each down wave's score-weighted rows
+  __shared__ float red_l[K][C::CROWS];                // the combine's per-rank rows
   __shared__ int sel_id[K];
   __shared__ float sel_sc[K];
   __shared__ int32_t sel_ref[K];
@@ -457,7 +534,7 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
   __shared__ uint32_t lstart;          // the layer boundary was seen (wave 7)
   __shared__ uint32_t routed;          // the routing and positions are known (wave 7)
   __shared__ uint32_t looked;          // layer l+1's prediction is in pred_* (wave 6)
-  __shared__ uint32_t hready[K];       // position p's activations polled (wave 4 + p)
+  __shared__ uint32_t hcnt;            // monotonic: WAVES_U per layer (activation quarters staged)
   // monotonic counters
   __shared__ uint32_t dsync;           // 8 arrivals per layer: every wave is done with it
   __shared__ uint32_t fsync;           // the gate/up waves' meetings in fix-ups
@@ -469,16 +546,20 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
   uint64_t *const lgt = reinterpret_cast<uint64_t *>(a.ws + WS::kLgt);
   uint64_t *const hpred = reinterpret_cast<uint64_t *>(a.ws + WS::kHpred);
   uint64_t *const hfix = reinterpret_cast<uint64_t *>(a.ws + WS::kHfix);
+  uint64_t *const part = reinterpret_cast<uint64_t *>(a.ws + WS::kPart);
   const bool uact = wg < C::ITEMS_U, dact = wg < C::ITEMS_D;
-  const int upos = min(wg / NPOS, K - 1), urow0 = (wg % NPOS) * ROWS_U;   // gate/up block
-  const int drow0 = dact ? wg * ROWS_D : 0;                                // down block
+  static_assert(C::ITEMS_U % K == 0 && C::ITEMS_D % K == 0 && C::ITEMS_U / K == NPOS,
+                "positions dealt round robin over the workgroups");
+  const int upos = wg % K, urow0 = (wg / K) * ROWS_U;            // gate/up block
+  const int drow0 = dact ? (wg / K) * C::ROWS_DWG : 0;           // down rows (position upos)
+  const int crow0 = dact ? wg * C::CROWS : 0;                    // combined output rows
+  constexpr int W_COMB = W_DMA + 1;   // combines the previous layer (idle until the routing)
   {
     const uint32_t none = layer_flag(a, 0) - 1u;   // no flag of this launch
     if (tid0 < 2) pred_cnt[tid0] = 0;   // layer 0 has no prediction
-    if (tid0 < K) hready[tid0] = none;
     if (tid0 == 0) {
       routed = lstart = looked = none;
-      dsync = fsync = staged = 0;
+      dsync = fsync = staged = hcnt = 0;
     }
   }
   __syncthreads();
@@ -536,27 +617,28 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
         lds_wait_count(&fsync, C::WAVES_U * ++nfs);
       }
       if (wave == 0) trace_mark(a, l, TR_FIXED);
-      // ---- gate/up wave p polls position p's activations and stages them
-      // for the down wave of that position: it has no loads in flight here,
-      // while the down waves' polls would return only after their
-      // direct-to-LDS down-row loads (loads complete in order)
+      // ---- gate/up wave w polls quarter w of the activations of the
+      // workgroup's position and stages it for the down waves: it has no
+      // loads in flight here, while the down waves' polls would return only
+      // after their direct-to-LDS down-row loads (loads complete in order)
       if (uact) {
-        const int p = wave;
-        const bool fix = pos_fix[p] >= 0;
-        uint4 pv[HPL];
-        get_acts_wide<HU4, HPL>(tid, (fix ? hfix : hpred) + (size_t)p * (F / 2), fl, ab, pv);
+        const bool fix = pos_fix[upos] >= 0;
+        uint4 pv[C::HPWL];
+        get_acts_quarter<HU4, C::HPW, C::HPWL>(tid, (fix ? hfix : hpred) + (size_t)upos * (F / 2),
+                                               wave, fl, ab, pv);
         if (dact) {
 #pragma unroll
-          for (int it = 0; it < HPL; ++it) {
-            const int i = lane + 64 * it;
+          for (int it = 0; it < C::HPWL; ++it) {
+            const int k = lane + 64 * it, i = C::HPW * wave + k;
+            const bool mine = k < C::HPW && i < HU4;
             float sm = 0.f;
-            if (i < HU4) sm = stage_piece<UF>(hact_l[p], i, pv[it]);
+            if (mine) sm = stage_piece<UF>(hact_l, i, pv[it]);
             sm += dpp_f<kDppQuadXor1>(sm);
             sm += dpp_f<kDppQuadXor2>(sm);
-            if (i < HU4 && (i & 3) == 0) hsum_l[p][i >> 2] = sm;
+            if (mine && (i & 3) == 0) hsum_l[i >> 2] = sm;
           }
         }
-        lds_set_flag(&hready[p], fl);
+        lds_arrive(&hcnt);
         if (wave == 2) trace_mark(a, l, TR_D_WAITED);
       }
       lds_arrive(&dsync);
@@ -567,8 +649,7 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
       // does when there is a next layer)
       if (has_next && uact) lds_wait_flag(&looked, fl);
       if (has_next && uact && upos < pred_cnt[(l + 1) & 1]) {
-#pragma unroll
-        for (int p = 0; p < K; ++p) lds_wait_flag(&hready[p], fl);
+        lds_wait_count(&hcnt, (uint32_t)C::WAVES_U * (uint32_t)(l + 1));
         ur.load(tid, a, pred_ref[(l + 1) & 1][upos], urow0, sbu_l, ubias_l);
       } else {
         ur.forget();
@@ -576,6 +657,13 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
     } else {
       ur.forget();
       if (wave < W_ROUTER) {
+        // wave 5: the previous layer's output rows, complete once its
+        // boundary is passed (the entries' flags confirm each)
+        if (wave == W_COMB && dact && l > 0) {
+          lds_wait_flag(&lstart, fl);
+          wide_combine<K, C::CROWS>(part + (size_t)((l - 1) & 1) * K * kStackMaxD, crow0,
+                                    layer_flag(a, l - 1), ab, red_l, KARG(y) + (size_t)(l - 1) * D);
+        }
         lds_wait_flag(&routed, fl);
       } else if (wave == W_ROUTER) {
         // ---- one router row (the lane partition and summation order of
@@ -766,49 +854,59 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
         }
         lds_set_flag(&routed, fl);
       }
-      // ---- wave 4 + p owns position p: its down rows into LDS by
-      // direct-to-LDS loads (issued once the routing is known), its down
-      // biases, then its activations polled and staged (every gate/up
-      // workgroup polls, so that its next-layer loads wait for the polls),
-      // then the down rows
-      const int p = wave - W_DMA;
-      const int r = pos_rank[p];
+      // ---- down wave q = wave - 4: 16 rows of the expert at the
+      // workgroup's position into LDS by direct-to-LDS loads (issued once
+      // the routing is known), its down biases, then (the activations
+      // staged by the gate/up waves) the rows, published as flagged entries
+      // of the expert's rank
+      const int q = wave - W_DMA;
+      const int r = pos_rank[upos];
       const int32_t dref = __builtin_amdgcn_readfirstlane(sel_ref[r]);
+      const int qrow0 = drow0 + q * ROWS_D;
       if (dact) {
-        wide_d_stage<C>(lane, a, dref, drow0, dcode_l[p], dsc_l[p]);
+        wide_d_stage<C>(lane, a, dref, qrow0, dcode_l[q], dsc_l[q]);
         if (PBIAS && lane < ROWS_D) {
           const uint16_t *dbias = reinterpret_cast<const uint16_t *>(resolve_packed<typename C::Layout>(
               a.pa, comp_index(PROJ_DOWN, PART_BIAS, NP), dref));
-          dbias_l[p][lane] = dbias ? bf16_to_f32(dbias[drow0 + lane]) : 0.f;
+          dbias_l[q][lane] = dbias ? bf16_to_f32(dbias[qrow0 + lane]) : 0.f;
         }
       }
       if (dact) {
         __builtin_amdgcn_s_waitcnt(0);   // this wave's direct-to-LDS loads landed
-        lds_wait_flag(&hready[p], fl);   // the activations, staged by gate/up wave p
+        lds_wait_count(&hcnt, (uint32_t)C::WAVES_U * (uint32_t)(l + 1));   // the activations
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        wide_down_rows<C>(lane, a, dref, sel_sc[r], dcode_l[p],
-                          reinterpret_cast<const uint16_t *>(&dsc_l[p][0][0]), hact_l[p], hsum_l[p],
-                          dbias_l[p], red_l[r]);
+        wide_down_rows<C>(lane, a, dref, sel_sc[r], dcode_l[q],
+                          reinterpret_cast<const uint16_t *>(&dsc_l[q][0][0]), hact_l, hsum_l,
+                          dbias_l[q], dred_l[q]);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_wave_barrier();
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (lane < ROWS_D)
+          __hip_atomic_store(part + ((size_t)(l & 1) * K + r) * kStackMaxD + qrow0 + lane,
+                             (uint64_t)__float_as_uint(dred_l[q][lane]) | ((uint64_t)fl << 32),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (wave == W_DMA) trace_mark(a, l, TR_LOGITS);   // (slot reused: down rows done)
       }
       lds_arrive(&dsync);
     }
-    // ---- wave 7: once every wave is done with layer l, combine in rank
-    // order, store, arrive.  Nothing in the launch reads y, and every entry
-    // this workgroup read in layer l has been read, so the arrival needs no
-    // wait for the stores: a workgroup past the boundary may overwrite them.
+    // ---- wave 7: once every wave is done with layer l, arrive.  Every
+    // entry this workgroup read in layer l has been read, and its per-rank
+    // output rows carry the layer's flag, so the arrival needs no wait for
+    // its stores.
     if (wave == W_RANK) {
       lds_wait_count(&dsync, 8u * (uint32_t)(l + 1));
-      if (dact && lane < ROWS_D) {
-        float yv = 0.f;
-        for (int w = 0; w < K; ++w) yv += red_l[w][lane];   // rank order
-        KARG(y)[(size_t)l * D + drow0 + lane] = (uint16_t)f32_to_bf16(yv);
-      }
       if (lane == 0)
         __hip_atomic_fetch_add(counter<WS>(a, l, CNT_D) + (wg % kSub) * 32, 1u,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       trace_mark(a, l, TR_D_ARRIVED);
     }
+  }
+  // the last layer's output rows, after every workgroup has arrived
+  if ((threadIdx.x >> 6) == W_RANK) {
+    wave_wait(counter<WS>(a, a.L - 1, CNT_D), ep * NWG, ab);
+    if (dact)
+      wide_combine<K, C::CROWS>(part + (size_t)((a.L - 1) & 1) * K * kStackMaxD, crow0,
+                                layer_flag(a, a.L - 1), ab, red_l, KARG(y) + (size_t)(a.L - 1) * D);
   }
 }
 
