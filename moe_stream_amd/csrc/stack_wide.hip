@@ -535,6 +535,8 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
   __shared__ uint32_t routed;          // the routing and positions are known (wave 7)
   __shared__ uint32_t looked;          // layer l+1's prediction is in pred_* (wave 6)
   __shared__ uint32_t hcnt;            // monotonic: WAVES_U per layer (activation quarters staged)
+  __shared__ uint32_t dpre;            // monotonic: 2 per layer (waves 4 and 5 done with the
+                                       // predicted expert's down rows)
   // monotonic counters
   __shared__ uint32_t dsync;           // 8 arrivals per layer: every wave is done with it
   __shared__ uint32_t fsync;           // the gate/up waves' meetings in fix-ups
@@ -559,7 +561,7 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
     if (tid0 < 2) pred_cnt[tid0] = 0;   // layer 0 has no prediction
     if (tid0 == 0) {
       routed = lstart = looked = none;
-      dsync = fsync = staged = hcnt = 0;
+      dsync = fsync = staged = hcnt = dpre = 0;
     }
   }
   __syncthreads();
@@ -659,11 +661,29 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
       if (wave < W_ROUTER) {
         // wave 5: the previous layer's output rows, complete once its
         // boundary is passed (the entries' flags confirm each)
-        if (wave == W_COMB && dact && l > 0) {
-          lds_wait_flag(&lstart, fl);
+        lds_wait_flag(&lstart, fl);
+        if (wave == W_COMB && dact && l > 0)
           wide_combine<K, C::CROWS>(part + (size_t)((l - 1) & 1) * K * kStackMaxD, crow0,
                                     layer_flag(a, l - 1), ab, red_l, KARG(y) + (size_t)(l - 1) * D);
+        // waves 4 and 5, idle until the routing: the down rows of the
+        // expert predicted at this position, all four quarters (wave 4
+        // quarters 0 and 2, wave 5 quarters 1 and 3), then an arrival once
+        // they landed
+        if (dact && upos < pred_cnt[l & 1]) {
+          const int32_t pref = __builtin_amdgcn_readfirstlane(pred_ref[l & 1][upos]);
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int qq = (wave - W_DMA) + 2 * h;
+            wide_d_stage<C>(lane, a, pref, drow0 + qq * ROWS_D, dcode_l[qq], dsc_l[qq]);
+            if (PBIAS && lane < ROWS_D) {
+              const uint16_t *dbias = reinterpret_cast<const uint16_t *>(resolve_packed<typename C::Layout>(
+                  a.pa, comp_index(PROJ_DOWN, PART_BIAS, NP), pref));
+              dbias_l[qq][lane] = dbias ? bf16_to_f32(dbias[drow0 + qq * ROWS_D + lane]) : 0.f;
+            }
+          }
+          __builtin_amdgcn_s_waitcnt(0);
         }
+        lds_arrive(&dpre);
         lds_wait_flag(&routed, fl);
       } else if (wave == W_ROUTER) {
         // ---- one router row (the lane partition and summation order of
@@ -863,7 +883,13 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
       const int r = pos_rank[upos];
       const int32_t dref = __builtin_amdgcn_readfirstlane(sel_ref[r]);
       const int qrow0 = drow0 + q * ROWS_D;
-      if (dact) {
+      // the rows staged by waves 4 and 5 at the layer start (their loads
+      // landed) are the routed expert's when the position kept its
+      // prediction; otherwise this wave stages its own, after those loads
+      // (they write the same LDS)
+      if (dact) lds_wait_count(&dpre, 2u * (uint32_t)(l + 1));
+      if (wave == W_DMA) trace_mark(a, l, TR_SOFTMAX);   // (slot reused: predicted rows in)
+      if (dact && !(upos < pred_cnt[l & 1] && pos_fix[upos] < 0)) {
         wide_d_stage<C>(lane, a, dref, qrow0, dcode_l[q], dsc_l[q]);
         if (PBIAS && lane < ROWS_D) {
           const uint16_t *dbias = reinterpret_cast<const uint16_t *>(resolve_packed<typename C::Layout>(
@@ -873,7 +899,9 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
       }
       if (dact) {
         __builtin_amdgcn_s_waitcnt(0);   // this wave's direct-to-LDS loads landed
+        if (wave == W_DMA) trace_mark(a, l, TR_LOOKED);   // (slot reused)
         lds_wait_count(&hcnt, (uint32_t)C::WAVES_U * (uint32_t)(l + 1));   // the activations
+        if (wave == W_DMA) trace_mark(a, l, TR_SPARE1);   // (slot reused)
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         wide_down_rows<C>(lane, a, dref, sel_sc[r], dcode_l[q],
                           reinterpret_cast<const uint16_t *>(&dsc_l[q][0][0]), hact_l, hsum_l,
@@ -886,6 +914,7 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
                              (uint64_t)__float_as_uint(dred_l[q][lane]) | ((uint64_t)fl << 32),
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (wave == W_DMA) trace_mark(a, l, TR_LOGITS);   // (slot reused: down rows done)
+        if (wave == W_RANK) trace_mark(a, l, TR_UROWS2);  // (slot reused)
       }
       lds_arrive(&dsync);
     }

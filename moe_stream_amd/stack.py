@@ -137,10 +137,12 @@ class DecodeStack:
     PERSISTENT = {(2048, 768, 8, False, _lib.MOE_ACT_SWIGLU, _lib.MOE_ROUTE_SOFTMAX_TOPK),
                   (2880, 2880, 4, True, _lib.MOE_ACT_SWIGLU_CLAMP, _lib.MOE_ROUTE_TOPK_SOFTMAX)}
 
-    # geometries whose whole-token kernel is the faster decode: the gpt-oss
-    # kernel is bit-exact but measured below the per-layer graph replay
-    # (about 1000 vs 1140 tokens/s over 36 layers on one MI355X)
-    PERSISTENT_PREFERRED = {(2048, 768, 8, False, _lib.MOE_ACT_SWIGLU, _lib.MOE_ROUTE_SOFTMAX_TOPK)}
+    # geometries whose whole-token kernel is the faster decode (both, on one
+    # MI355X: Qwen3 48 layers about 1,900 against 1,150 tokens/s for the
+    # per-layer graph; gpt-oss 36 layers 1,158-1,179 against 1,096-1,120)
+    PERSISTENT_PREFERRED = {(2048, 768, 8, False, _lib.MOE_ACT_SWIGLU, _lib.MOE_ROUTE_SOFTMAX_TOPK),
+                            (2880, 2880, 4, True, _lib.MOE_ACT_SWIGLU_CLAMP,
+                             _lib.MOE_ROUTE_TOPK_SOFTMAX)}
 
     def persistent_preferred(self) -> bool:
         g = self.geom
