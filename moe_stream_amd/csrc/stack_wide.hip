@@ -22,8 +22,10 @@
 //   routing  wave 7: the layer boundary, x staged in LDS, the ranking of
 //            the routed experts, which position holds which rank
 //   fix-up   a routed expert that was not predicted takes the position of a
-//            predicted expert that was not routed: that position's gate/up
-//            rows and down rows are loaded once the routing is known
+//            predicted expert that was not routed: its gate/up rows are
+//            spread over the whole grid (two rows per gate/up wave and task,
+//            straight from the pool) and its down rows are staged by that
+//            position's down waves once the routing is known
 //   D        the four gate/up waves collect a quarter each of the
 //            activations of the workgroup's position into LDS (they have no
 //            loads in flight, so their polls return at once); waves 4-7 run
@@ -398,6 +400,82 @@ struct WideU {
   }
 };
 
+// One whole wave: fix-up task t of expert `ref`, i.e. its gate/up rows 2t
+// (lanes 0-31) and 2t + 1 (lanes 32-63) straight from the pool, published as
+// the flagged entry hf[t].  The lane partition, the chunk order and the
+// arithmetic are WideU::run's for one step, so a row computed here is
+// bit-identical to the same row computed by its position's workgroup.
+template <class C>
+__device__ __forceinline__ void wide_fix_task(int lane, const StackArgs &a, int32_t ref, int t,
+                                              const uint4 *act_l, const float *asum_l,
+                                              uint64_t *hf, uint32_t fl) {
+  constexpr int D = C::D_, U = C::U, NG = C::NG, SGU = C::SGU, CPLU = C::CPLU, NP = C::NP;
+  using Lay = typename C::Layout;
+  const int uj = lane % SGU, usub = lane / SGU;
+  const int row = 2 * t + usub;
+  ref = __builtin_amdgcn_readfirstlane(ref);
+  bool ok;
+  const char *gw = resolve_packed_safe<Lay>(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
+  const char *uw = resolve_packed_safe<Lay>(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
+  const uint16_t *sp[4] = {
+      reinterpret_cast<const uint16_t *>(resolve_packed_safe<Lay>(a.pa, comp_index(PROJ_GATE, PART_S, NP), ref, ok)),
+      reinterpret_cast<const uint16_t *>(resolve_packed_safe<Lay>(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok)),
+      reinterpret_cast<const uint16_t *>(resolve_packed_safe<Lay>(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok)),
+      reinterpret_cast<const uint16_t *>(resolve_packed_safe<Lay>(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok))};
+  // every load unconditional (surplus chunks re-read the last one, unused)
+  uint32_t sv[4][CPLU];
+#pragma unroll
+  for (int i = 0; i < CPLU; ++i) {
+    const int g = row * NG + (min(i * SGU + uj, U - 1) >> 1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sv[j][i] = sp[j][g];
+  }
+  float gbv = 0.f, ubv = 0.f;
+  if (C::PBIAS_) {
+    bool okb;
+    gbv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
+        resolve_packed_safe<Lay>(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[row]);
+    ubv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
+        resolve_packed_safe<Lay>(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[row]);
+  }
+  uint4 cg[CPLU], cu[CPLU];
+#pragma unroll
+  for (int i = 0; i < CPLU; ++i) {
+    const uint32_t off = (uint32_t)(row * (D / 2) + min(i * SGU + uj, U - 1) * 16);
+    cg[i] = load_stream16(reinterpret_cast<const uint4 *>(gw + off));
+    cu[i] = load_stream16(reinterpret_cast<const uint4 *>(uw + off));
+  }
+  float pg = 0.f, pu = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPLU; ++i) {
+    const int c = i * SGU + uj;
+    if (CPLU * SGU == U || c < U) {
+      uint4 xa[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) xa[q] = act_l[q * U + c];
+      const float xs = asum_l[c];
+      const float Sg = bf16_to_f32(sv[0][i]), Bg = bf16_to_f32(sv[1][i]);
+      const float Su = bf16_to_f32(sv[2][i]), Bu = bf16_to_f32(sv[3][i]);
+      pg += Sg * chunk_dot_regs(cg[i], xa) + (Bg - 128.f * Sg) * xs;
+      pu += Su * chunk_dot_regs(cu[i], xa) + (Bu - 128.f * Su) * xs;
+    }
+  }
+  float g = group_sum<SGU>(pg);
+  float u = group_sum<SGU>(pu);
+  if (C::PBIAS_) {
+    g += gbv;
+    u += ubv;
+  }
+  uint32_t hb = 0;
+  if (ok) hb = f32_to_bf16(wide_act<C>(g, u));
+  else if (lane == 0) flag_error();
+  static_assert(C::RPSU == 2, "two rows per task");
+  const uint32_t h0 = __builtin_amdgcn_readlane(hb, 0), h1 = __builtin_amdgcn_readlane(hb, 32);
+  if (lane == 0)
+    __hip_atomic_store(hf + t, (uint64_t)(h0 | (h1 << 16)) | ((uint64_t)fl << 32),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // One whole wave: the down rows of expert `ref` for this workgroup's 16-row
 // block into the LDS image of one position by direct-to-LDS loads: codes as
 // [step][chunk][lane] (the lane's 16 bytes of row step * 4 + lane / 16),
@@ -468,19 +546,46 @@ __device__ __forceinline__ void wide_down_rows(int lane, const StackArgs &a, int
   float pv[RS];
 #pragma unroll
   for (int st = 0; st < RS; ++st) pv[st] = 0.f;
+  // A software pipeline over the (chunk, row) steps: the code word and the
+  // scales of step n + 1 are read while step n computes, and the next
+  // chunk's activations during the chunk's last row, so the LDS latency
+  // hides behind a row of arithmetic instead of a wait before every row.
+  // Lanes past the last chunk read a clamped (valid) chunk and add nothing.
+  uint4 xa[2][4], cd[2];
+  uint32_t sv[2], bv[2];
+  float xs[2];
+  auto fetch_x = [&](int i, int b) {
+    const int c = min(i * SGD + dj, UF - 1);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xa[b][q] = hact[q * UF + c];
+    xs[b] = hsum[c];
+  };
+  auto fetch_row = [&](int i, int st, int b) {
+    const int c = min(i * SGD + dj, UF - 1);
+    const int g = (st * RPSD + dsub) * NGF + (c >> 1);
+    cd[b] = code[st * CPLD + i][lane];
+    sv[b] = sbh[g];
+    bv[b] = sbh[SBN + g];
+  };
+  fetch_x(0, 0);
+  fetch_row(0, 0, 0);
 #pragma unroll
   for (int i = 0; i < CPLD; ++i) {
     const int c = i * SGD + dj;
-    if (CPLD * SGD == UF || c < UF) {
-      uint4 xa[4];
+    const bool in = CPLD * SGD == UF || c < UF;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) xa[q] = hact[q * UF + c];
-      const float xs = hsum[c];
-#pragma unroll
-      for (int st = 0; st < RS; ++st) {
-        const int g = (st * RPSD + dsub) * NGF + (c >> 1);
-        const float Sd = bf16_to_f32(sbh[g]), Bd = bf16_to_f32(sbh[SBN + g]);
-        pv[st] += Sd * chunk_dot_regs(code[st * CPLD + i][lane], xa) + (Bd - 128.f * Sd) * xs;
+    for (int st = 0; st < RS; ++st) {
+      const int n = i * RS + st, b = n & 1;
+      if (st + 1 < RS) fetch_row(i, st + 1, b ^ 1);
+      else if (i + 1 < CPLD) {
+        fetch_row(i + 1, 0, b ^ 1);
+        fetch_x(i + 1, (i + 1) & 1);
+      }
+      // (the scheduler would otherwise sink the reads next to their use)
+      __builtin_amdgcn_sched_barrier(0);
+      if (in) {
+        const float Sd = bf16_to_f32(sv[b]), Bd = bf16_to_f32(bv[b]);
+        pv[st] += Sd * chunk_dot_regs(cd[b], xa[i & 1]) + (Bd - 128.f * Sd) * xs[i & 1];
       }
     }
   }
@@ -524,6 +629,8 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
   __shared__ int pred_cnt[2];          // predicted positions (<= K)
   __shared__ int pos_fix[K];           // position p runs a fix-up of this rank, or -1
   __shared__ int pos_rank[K];          // routing rank whose activations position p holds
+  __shared__ int fix_pos[K];           // the positions running a fix-up, in order
+  __shared__ int n_fix;                // ... how many
   // monotonic: WAVES_U + 1 arrivals per layer (the gate/up waves' loads
   // landed, x staged); layer l's meeting waits for (WAVES_U + 1) * (l + 1).
   // A wave arrives for layer l + 1 only after layer l's meeting (gate/up
@@ -539,7 +646,6 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
                                        // predicted expert's down rows)
   // monotonic counters
   __shared__ uint32_t dsync;           // 8 arrivals per layer: every wave is done with it
-  __shared__ uint32_t fsync;           // the gate/up waves' meetings in fix-ups
 
   const int tid0 = threadIdx.x;
   const int wg = blockIdx.x;
@@ -561,14 +667,13 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
     if (tid0 < 2) pred_cnt[tid0] = 0;   // layer 0 has no prediction
     if (tid0 == 0) {
       routed = lstart = looked = none;
-      dsync = fsync = staged = hcnt = dpre = 0;
+      dsync = staged = hcnt = dpre = 0;
     }
   }
   __syncthreads();
 
   // gate/up registers of the predicted expert, loaded one layer ahead
   WideU<C> ur = {};
-  uint32_t nfs = 0;   // fix-up meetings so far (gate/up waves)
 
   // Roles per layer, ordered by LDS flags and counters rather than
   // workgroup barriers: a wave issuing a large batch of loads is held at its
@@ -603,20 +708,21 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
         KARG(refs_out)[(size_t)l * K + tid] = sel_ref[tid];
         if (sel_ref[tid] < 0) atomicAdd(KARG(miss) + l, 1);
       }
-      // ---- fix-up: this position's predicted expert was not routed; it
-      // takes a routed expert that was not predicted (its down rows are
-      // staged by waves 4 and 5 like the others)
-      const int fu = uact ? pos_fix[upos] : -1;   // uniform over the workgroup
-      if (fu >= 0) {
-        ur.load(tid, a, sel_ref[fu], urow0, sbu_l, ubias_l);
-        __builtin_amdgcn_s_waitcnt(0);
-        lds_arrive(&fsync);
-        lds_wait_count(&fsync, C::WAVES_U * ++nfs);
-        ur.run(tid, act_l, asum_l, reinterpret_cast<const uint16_t *>(sbu_l),
-               reinterpret_cast<const uint16_t *>(ubias_l), hfix + (size_t)upos * (F / 2),
-               urow0, fl);
-        lds_arrive(&fsync);   // the scales and biases are read before the next loads land
-        lds_wait_count(&fsync, C::WAVES_U * ++nfs);
+      // ---- fix-up: a position whose predicted expert was not routed takes
+      // a routed expert that was not predicted.  Its gate/up rows are spread
+      // over the whole grid (task t = wave * NWG + workgroup: rows 2t, 2t+1
+      // of the fix-up in t / (F / 2)), straight from the pool, so one miss
+      // costs each gate/up wave about one task instead of a 48-row pass on
+      // the position's own workgroups (its down rows are staged by its down
+      // waves like the others)
+      {
+        constexpr int FT = F / 2;
+        const int nf = n_fix;
+        for (int t = wave * NWG + wg; t < nf * FT; t += C::WAVES_U * NWG) {
+          const int p = fix_pos[t / FT];
+          wide_fix_task<C>(lane, a, sel_ref[pos_rank[p]], t % FT, act_l, asum_l,
+                           hfix + (size_t)p * (F / 2), fl);
+        }
       }
       if (wave == 0) trace_mark(a, l, TR_FIXED);
       // ---- gate/up wave w polls quarter w of the activations of the
@@ -858,6 +964,8 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
         }
         const uint64_t free_m = __ballot(lane < K && prank < 0);   // positions needing a fix-up
         const uint64_t miss_m = __ballot(lane < K && !hit);         // ranks needing a fix-up
+        if (lane < K && prank < 0) fix_pos[__popcll(free_m & below)] = lane;
+        if (lane == 0) n_fix = __popcll(free_m);
         if (lane < K) {
           if (prank >= 0) {
             pos_rank[lane] = prank;
