@@ -216,6 +216,25 @@ def test_grouped_token_order_residency_and_determinism(qwen_layer):
     assert torch.equal(ym, y1)
 
 
+def test_grouped_repeated_calls_with_mixed_tile_keys_bit_identical(qwen_layer):
+    """A key with one full 64-row tile and a small remainder tile: the
+    grouping scatters its pairs over the two tiles in a different order every
+    call (its scatter cursors are atomics), and the outputs stay
+    bit-identical: a row's result does not depend on the tile it lands in."""
+    g = qwen_layer.geom
+    T = 76
+    rng = np.random.default_rng(20260053)
+    ids = np.stack([np.concatenate([[7], rng.permutation(np.arange(8, 128))[:g.top_k - 1]])
+                    for _ in range(T)])   # expert 7 in every token: 76 pairs = 64 + 12
+    refs = torch.tensor(qwen_layer.perm[ids], dtype=torch.int32, device="cuda")
+    sc = torch.tensor(rng.dirichlet(np.ones(g.top_k), T).astype(np.float32), device="cuda")
+    x = bf16_randn((T, 2048), seed=20260054)
+    ys = [ops.ffn_grouped(qwen_layer.pool, refs, sc, x) for _ in range(4)]
+    torch.cuda.synchronize()
+    for y in ys[1:]:
+        assert torch.equal(y, ys[0])
+
+
 @pytest.mark.parametrize("T,k,rows_per_expert", [(1, 4, None), (17, 4, None),
                                                  (64, 1, 64), (65, 1, 65), (130, 2, None)])
 def test_grouped_ragged_tiles_small_geometry(T, k, rows_per_expert):
