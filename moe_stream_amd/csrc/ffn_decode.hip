@@ -617,7 +617,7 @@ __global__ __launch_bounds__(NW * 64) void ffn_down_small_kernel(
   constexpr int NG = LY::NG, NP = PBIAS ? 4 : 3, SB_U4 = LY::SB_U4, HU4 = F / 8;
   constexpr int HIT = (HU4 + 63) / 64, SIT = (2 * SB_U4 + 63) / 64;
   constexpr int NC = kSmallMaxPairs / 64;
-  constexpr int MBD = HIT <= 2 ? 4 : 2;   // member activations loaded together
+  constexpr int MBD = HIT <= 2 ? 4 : HIT <= 4 ? 2 : 1;   // member activations loaded together
   extern __shared__ uint4 dyn_lds[];
   const int rb = blockIdx.x, row0 = rb * ROWS_WG;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
