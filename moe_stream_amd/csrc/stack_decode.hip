@@ -209,9 +209,10 @@ struct Abort {
 
 // One whole wave: poll until the counter's sum >= target (no barrier).
 // Bounded: past the spin limit, or as soon as any workgroup has flagged an
-// error, it gives up (wrong results, never a hang).
-__device__ __forceinline__ void wave_wait(const uint32_t *c, uint32_t target, const Abort &ab) {
-  const int lane = threadIdx.x & 63;
+// error, it gives up (wrong results, never a hang).  `lane`: the caller's
+// lane index (a kernel may pass one it keeps from being hoisted).
+__device__ __forceinline__ void wave_wait(const uint32_t *c, uint32_t target, const Abort &ab,
+                                          int lane) {
   uint32_t spins = 0;
   while (true) {
     int v = (lane < kSub) ? (int)__hip_atomic_load(c + lane * 32, __ATOMIC_RELAXED,
@@ -227,13 +228,16 @@ __device__ __forceinline__ void wave_wait(const uint32_t *c, uint32_t target, co
     __builtin_amdgcn_s_sleep(1);
   }
 }
+__device__ __forceinline__ void wave_wait(const uint32_t *c, uint32_t target, const Abort &ab) {
+  wave_wait(c, target, ab, threadIdx.x & 63);
+}
 
 // One whole wave: the logits of entries lane and lane + 64 of `slots` (n
 // entries, n <= 128), polled until every present entry carries `fl`.
 // Bounded like wave_wait.
 __device__ __forceinline__ void get_logits(const uint64_t *slots, int n, uint32_t fl,
-                                           const Abort &ab, float &z0, float &z1) {
-  const int lane = threadIdx.x & 63, e0 = lane, e1 = lane + 64;
+                                           const Abort &ab, float &z0, float &z1, int lane) {
+  const int e0 = lane, e1 = lane + 64;
   const uint64_t *p0 = slots + min(e0, n - 1), *p1 = slots + min(e1, n - 1);
   uint32_t spins = 0;
   while (true) {
@@ -246,6 +250,10 @@ __device__ __forceinline__ void get_logits(const uint64_t *slots, int n, uint32_
     if (ab.gave_up(++spins)) break;
     __builtin_amdgcn_s_sleep(1);
   }
+}
+__device__ __forceinline__ void get_logits(const uint64_t *slots, int n, uint32_t fl,
+                                           const Abort &ab, float &z0, float &z1) {
+  get_logits(slots, n, fl, ab, z0, z1, threadIdx.x & 63);
 }
 
 // All threads of the workgroup: wait until the counter's sum >= target.

@@ -220,6 +220,16 @@ __device__ __forceinline__ void get_acts_quarter(int tid, const uint64_t *hf, in
   }
 }
 
+// The lane index, made opaque at each use: what is derived from it (LDS and
+// global addresses, lane-0 masks) is computed where it is used instead of
+// being held in registers across the layer loop (this kernel runs at the
+// register limit, and values held that way are spilled to scratch).
+__device__ __forceinline__ int wide_lane() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t & 63;
+}
+
 // One whole wave (lane = rank * CROWS + row): the layer's combined output
 // rows [crow0, crow0 + CROWS) from the K per-rank flagged entries of `part`
 // (polled until each carries `fl`), summed in rank order through `red`.
@@ -227,7 +237,7 @@ template <int K, int CROWS>
 __device__ __forceinline__ void wide_combine(const uint64_t *part, int crow0, uint32_t fl,
                                              const Abort &ab, float (*red)[CROWS],
                                              uint16_t *y) {
-  const int lane = threadIdx.x & 63;
+  const int lane = wide_lane();
   const int r = min(lane / CROWS, K - 1), i = lane % CROWS;
   const bool mine = lane < K * CROWS;
   const uint64_t *e = part + (size_t)r * kStackMaxD + crow0 + i;
@@ -252,7 +262,7 @@ __device__ __forceinline__ void wide_combine(const uint64_t *part, int crow0, ui
 // One whole wave: wait until the LDS word `w` holds `fl` (set by another
 // wave of the workgroup, which always sets it).
 __device__ __forceinline__ void lds_wait_flag(const uint32_t *w, uint32_t fl) {
-  if ((threadIdx.x & 63) == 0) {
+  if (wide_lane() == 0) {
     while (__hip_atomic_load(w, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != fl)
       __builtin_amdgcn_s_sleep(1);
   }
@@ -261,7 +271,7 @@ __device__ __forceinline__ void lds_wait_flag(const uint32_t *w, uint32_t fl) {
 }
 __device__ __forceinline__ void lds_set_flag(uint32_t *w, uint32_t fl) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  if ((threadIdx.x & 63) == 0) __hip_atomic_store(w, fl, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+  if (wide_lane() == 0) __hip_atomic_store(w, fl, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // Gate/up rows of expert `ref` for this workgroup's 48-row block, per wave
@@ -512,13 +522,13 @@ __device__ __forceinline__ void wide_d_stage(int lane, const StackArgs &a, int32
 // accesses before it.
 __device__ __forceinline__ void lds_arrive(uint32_t *c) {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  if ((threadIdx.x & 63) == 0)
+  if (wide_lane() == 0)
     __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 // One wave: wait until the monotonic LDS counter reaches `target` (its
 // arrivals are made by waves that always make them).
 __device__ __forceinline__ void lds_wait_count(const uint32_t *c, uint32_t target) {
-  if ((threadIdx.x & 63) == 0) {
+  if (wide_lane() == 0) {
     while ((int32_t)(__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) -
                      target) < 0)
       __builtin_amdgcn_s_sleep(1);
@@ -840,7 +850,7 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
           const int32_t *tabn = KARG(table) + (size_t)(l + 1) * a.E;
           const int32_t t0 = tabn[min(e0, a.E - 1)], t1 = tabn[min(e1, a.E - 1)];
           float l0, l1;
-          get_logits(lgt + a.E, a.E, fl, ab, l0, l1);
+          get_logits(lgt + a.E, a.E, fl, ab, l0, l1, wide_lane());
           const float z0 = e0 < a.E ? round_bf16(l0 + b0) : -INFINITY;
           const float z1 = e1 < a.E ? round_bf16(l1 + b1) : -INFINITY;
           bool s0, s1;
@@ -869,7 +879,7 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
         lds_wait_flag(&routed, fl);
       } else {
         // ---- the layer boundary, x_l into LDS, the routing -------------
-        if (l > 0) wave_wait(counter<WS>(a, l - 1, CNT_D), ep * NWG, ab);
+        if (l > 0) wave_wait(counter<WS>(a, l - 1, CNT_D), ep * NWG, ab, wide_lane());
         lds_set_flag(&lstart, fl);
         trace_mark(a, l, TR_R_WAITED);
         {
@@ -897,7 +907,7 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
         const int32_t *tab = KARG(table) + (size_t)l * a.E;
         const int32_t t0 = tab[min(e0, a.E - 1)], t1 = tab[min(e1, a.E - 1)];
         float l0, l1;
-        get_logits(lgt, a.E, fl, ab, l0, l1);
+        get_logits(lgt, a.E, fl, ab, l0, l1, wide_lane());
         trace_mark(a, l, TR_R_ALL);
         const float z0 = e0 < a.E ? round_bf16(l0 + b0) : -INFINITY;
         const float z1 = e1 < a.E ? round_bf16(l1 + b1) : -INFINITY;
