@@ -719,9 +719,13 @@ __device__ __forceinline__ void grouped_item(
   if (STAGE) {   // whole rows out, 16 bytes per lane
     constexpr int CPR = NB * OB / 16;                     // 16-byte chunks per row
     constexpr int EPC = 16 / OB;                          // elements per chunk
+    // (the thread index made opaque: the LDS addresses below are computed
+    // here, not held in registers across the work items)
+    int tid_e = tid;
+    asm volatile("" : "+v"(tid_e));
 #pragma unroll 1
     for (int it = 0; it < (ROWS * CPR + NT - 1) / NT; ++it) {
-      const int i = tid + NT * it, r = i / CPR, c = i % CPR;
+      const int i = tid_e + NT * it, r = i / CPR, c = i % CPR;
       if (i < ROWS * CPR && r < rows) {
         const int ec = (c * EPC) ^ (((r >> 2) & 3) << 4);
         const uint4 v = *reinterpret_cast<const uint4 *>(tile + (r * NB + ec) * OB);
