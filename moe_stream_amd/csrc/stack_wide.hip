@@ -13,9 +13,9 @@
 //            workgroup's position w % K (60 workgroups per position), held
 //            in the registers of waves 0-3 (one per SIMD, 12 rows each); the
 //            next layer's are loaded as soon as this layer's gate/up is done
-//   down     180 workgroups x 64 output rows of the expert at their position
-//            w % K (45 workgroups per position, 16 rows per down wave),
-//            staged in LDS (108 KiB of codes and scales) by direct-to-LDS
+//   down     240 workgroups x 48 output rows of the expert at their position
+//            w % K (60 workgroups per position, 12 rows per down wave),
+//            staged in LDS (84 KiB of codes and scales) by direct-to-LDS
 //            loads of waves 4-7 once the routing is known
 //   router   wave 6: one router row (+ the lookahead row), then the
 //            lookahead ranking of layer l+1
@@ -62,14 +62,20 @@ struct WideCfg {
   static constexpr int SB_U4 = ROWS_U * NG * 2 / 16;   // 16-byte pieces per scale array
   static constexpr int SUI_ALL = (4 * SB_U4 + 63) / 64;  // scale loads (1 KiB each)
   static constexpr int SUI = (SUI_ALL + WAVES_U - 1) / WAVES_U;   // per gate/up wave
-  // down: 16 lanes per row, 4 rows per unit, 4 units per position
+  // down: 16 lanes per row, 4 rows per step, 3 steps per wave (12 rows), 4
+  // waves per workgroup: 48 rows, so the K positions' rows take 240
+  // workgroups (as gate/up does) instead of 180 at 16 rows per wave
   static constexpr int UF = F / 32, NGF = F / 64;
   static constexpr int SGD = 16, CPLD = (UF + SGD - 1) / SGD, RPSD = 64 / SGD;
-  static constexpr int RSTEPS_D = 4, ROWS_D = RSTEPS_D * RPSD;   // rows per down wave
+  static constexpr int RSTEPS_D = 3, ROWS_D = RSTEPS_D * RPSD;   // rows per down wave
   static constexpr int WAVES_D = 4, ROWS_DWG = WAVES_D * ROWS_D;   // rows per workgroup
   static constexpr int ITEMS_D = K * (D / ROWS_DWG);               // down workgroups
   static constexpr int CROWS = D / ITEMS_D;                         // combined rows per workgroup
-  static constexpr int SBD_U4 = ROWS_D * NGF * 2 / 16;
+  // a down wave's scales (ROWS_D * NGF halfwords per array) start 8-byte
+  // aligned: its image is the 16-byte pieces from the aligned address below,
+  // one piece more than the rows need (the halfword offset DOFF(row0) skips
+  // the lead-in)
+  static constexpr int SBD_U4 = (ROWS_D * NGF * 2 + 8 + 15) / 16;
   static constexpr int DCI = RSTEPS_D * CPLD;          // code loads per position (1 KiB each)
   static constexpr int DSI = (2 * SBD_U4 + 63) / 64;   // scale loads per position
   static constexpr int NP = PBIAS ? 4 : 3;
@@ -81,7 +87,11 @@ struct WideCfg {
   static_assert(F % ROWS_U == 0 && D % ROWS_DWG == 0 && D % ITEMS_D == 0, "row blocks");
   static_assert(K * CROWS <= 64 && WAVES_U * HPW >= HU4, "combine lanes, activation quarters");
   static_assert(ITEMS_U <= NWG && ITEMS_D <= NWG, "one item per workgroup");
-  static_assert((ROWS_U * NG * 2) % 16 == 0 && (ROWS_D * NGF * 2) % 16 == 0, "scale pieces");
+  static_assert((ROWS_U * NG * 2) % 16 == 0 && (ROWS_D * NGF * 2) % 8 == 0, "scale pieces");
+  // the last wave's image ends inside the scale array
+  static_assert((((D - ROWS_D) * NGF * 2) & ~15) + SBD_U4 * 16 <= D * NGF * 2, "scale image");
+  // halfword offset of row row0's scales in its wave's image
+  static __device__ __forceinline__ int doff(int row0) { return (row0 * NGF) & 7; }
   static_assert(K == 4 && WAVES_U == 4 && NT / 64 == 8,
                 "a down wave per position beside each gate/up wave; two positions per staging wave");
 };
@@ -486,7 +496,7 @@ __device__ __forceinline__ void wide_fix_task(int lane, const StackArgs &a, int3
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// One whole wave: the down rows of expert `ref` for this workgroup's 16-row
+// One whole wave: the down rows of expert `ref` for one down wave's 12-row
 // block into the LDS image of one position by direct-to-LDS loads: codes as
 // [step][chunk][lane] (the lane's 16 bytes of row step * 4 + lane / 16),
 // then the scale and bias arrays' pieces (S | B).
@@ -501,11 +511,12 @@ __device__ __forceinline__ void wide_d_stage(int lane, const StackArgs &a, int32
   const char *dw = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_W, NP), ref, ok);
   const char *ds = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_S, NP), ref, ok);
   const char *db = resolve_packed_safe<typename C::Layout>(a.pa, comp_index(PROJ_DOWN, PART_B, NP), ref, ok);
+  const int64_t sb0 = ((int64_t)drow0 * NGF * 2) & ~(int64_t)15;   // 16-byte aligned
 #pragma unroll
   for (int it = 0; it < C::DSI; ++it) {
     const int i = min(it * 64 + lane, 2 * SBD_U4 - 1);
     const int p = i / SBD_U4, o = i % SBD_U4;
-    dma16(reinterpret_cast<const uint4 *>((p ? db : ds) + (int64_t)drow0 * NGF * 2) + o, &sc[it][0]);
+    dma16(reinterpret_cast<const uint4 *>((p ? db : ds) + sb0) + o, &sc[it][0]);
   }
 #pragma unroll
   for (int st = 0; st < C::RSTEPS_D; ++st) {
@@ -537,14 +548,14 @@ __device__ __forceinline__ void lds_wait_count(const uint32_t *c, uint32_t targe
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// The down rows of position p for this workgroup's 16-row block, from the
-// LDS images (codes and scales staged by direct-to-LDS loads, activations
-// and biases staged by the polling waves), chunk-outer: a chunk's
-// activations are read once for the 4 steps, and each row still sums its
+// The down rows of position p for one down wave's 12-row block (rows
+// row0...), from the LDS images (codes and scales staged by direct-to-LDS
+// loads, activations and biases staged by the polling waves), chunk-outer: a
+// chunk's activations are read once for the 3 steps, and each row still sums its
 // chunks in ascending order.  Writes the score-weighted rows to red.
 template <class C>
 __device__ __forceinline__ void wide_down_rows(int lane, const StackArgs &a, int32_t dref,
-                                               float sc, const uint4 (*code)[64],
+                                               int row0, float sc, const uint4 (*code)[64],
                                                const uint16_t *sbh, const uint4 *hact,
                                                const float *hsum, const float *dbias,
                                                float *red) {
@@ -572,7 +583,7 @@ __device__ __forceinline__ void wide_down_rows(int lane, const StackArgs &a, int
   };
   auto fetch_row = [&](int i, int st, int b) {
     const int c = min(i * SGD + dj, UF - 1);
-    const int g = (st * RPSD + dsub) * NGF + (c >> 1);
+    const int g = C::doff(row0) + (st * RPSD + dsub) * NGF + (c >> 1);
     cd[b] = code[st * CPLD + i][lane];
     sv[b] = sbh[g];
     bv[b] = sbh[SBN + g];
@@ -992,7 +1003,7 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
         }
         lds_set_flag(&routed, fl);
       }
-      // ---- down wave q = wave - 4: 16 rows of the expert at the
+      // ---- down wave q = wave - 4: 12 rows of the expert at the
       // workgroup's position into LDS by direct-to-LDS loads (issued once
       // the routing is known), its down biases, then (the activations
       // staged by the gate/up waves) the rows, published as flagged entries
@@ -1021,7 +1032,7 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
         lds_wait_count(&hcnt, (uint32_t)C::WAVES_U * (uint32_t)(l + 1));   // the activations
         if (wave == W_DMA) trace_mark(a, l, TR_SPARE1);   // (slot reused)
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        wide_down_rows<C>(lane, a, dref, sel_sc[r], dcode_l[q],
+        wide_down_rows<C>(lane, a, dref, qrow0, sel_sc[r], dcode_l[q],
                           reinterpret_cast<const uint16_t *>(&dsc_l[q][0][0]), hact_l, hsum_l,
                           dbias_l[q], dred_l[q]);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
