@@ -426,15 +426,24 @@ struct WideU {
 // arithmetic are WideU::run's for one step, so a row computed here is
 // bit-identical to the same row computed by its position's workgroup.
 template <class C>
-__device__ __forceinline__ void wide_fix_task(int lane, const StackArgs &a, int32_t ref, int t,
-                                              const uint4 *act_l, const float *asum_l,
-                                              uint64_t *hf, uint32_t fl) {
+struct WideFix {   // one fix-up task's operands in registers
+  uint32_t sv[4][C::CPLU];
+  uint4 cg[C::CPLU], cu[C::CPLU];
+  float gbv, ubv;
+  bool ok;
+};
+
+// The loads of task t (every load unconditional: surplus chunks re-read the
+// last one, unused).
+template <class C>
+__device__ __forceinline__ void wide_fix_load(int lane, const StackArgs &a, int32_t ref, int t,
+                                              WideFix<C> &o) {
   constexpr int D = C::D_, U = C::U, NG = C::NG, SGU = C::SGU, CPLU = C::CPLU, NP = C::NP;
   using Lay = typename C::Layout;
   const int uj = lane % SGU, usub = lane / SGU;
   const int row = 2 * t + usub;
   ref = __builtin_amdgcn_readfirstlane(ref);
-  bool ok;
+  bool ok = true;
   const char *gw = resolve_packed_safe<Lay>(a.pa, comp_index(PROJ_GATE, PART_W, NP), ref, ok);
   const char *uw = resolve_packed_safe<Lay>(a.pa, comp_index(PROJ_UP, PART_W, NP), ref, ok);
   const uint16_t *sp[4] = {
@@ -442,29 +451,39 @@ __device__ __forceinline__ void wide_fix_task(int lane, const StackArgs &a, int3
       reinterpret_cast<const uint16_t *>(resolve_packed_safe<Lay>(a.pa, comp_index(PROJ_GATE, PART_B, NP), ref, ok)),
       reinterpret_cast<const uint16_t *>(resolve_packed_safe<Lay>(a.pa, comp_index(PROJ_UP, PART_S, NP), ref, ok)),
       reinterpret_cast<const uint16_t *>(resolve_packed_safe<Lay>(a.pa, comp_index(PROJ_UP, PART_B, NP), ref, ok))};
-  // every load unconditional (surplus chunks re-read the last one, unused)
-  uint32_t sv[4][CPLU];
 #pragma unroll
   for (int i = 0; i < CPLU; ++i) {
     const int g = row * NG + (min(i * SGU + uj, U - 1) >> 1);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) sv[j][i] = sp[j][g];
+    for (int j = 0; j < 4; ++j) o.sv[j][i] = sp[j][g];
   }
-  float gbv = 0.f, ubv = 0.f;
+  o.gbv = 0.f;
+  o.ubv = 0.f;
   if (C::PBIAS_) {
     bool okb;
-    gbv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
+    o.gbv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
         resolve_packed_safe<Lay>(a.pa, comp_index(PROJ_GATE, PART_BIAS, NP), ref, okb))[row]);
-    ubv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
+    o.ubv = bf16_to_f32(reinterpret_cast<const uint16_t *>(
         resolve_packed_safe<Lay>(a.pa, comp_index(PROJ_UP, PART_BIAS, NP), ref, okb))[row]);
   }
-  uint4 cg[CPLU], cu[CPLU];
 #pragma unroll
   for (int i = 0; i < CPLU; ++i) {
     const uint32_t off = (uint32_t)(row * (D / 2) + min(i * SGU + uj, U - 1) * 16);
-    cg[i] = load_stream16(reinterpret_cast<const uint4 *>(gw + off));
-    cu[i] = load_stream16(reinterpret_cast<const uint4 *>(uw + off));
+    o.cg[i] = load_stream16(reinterpret_cast<const uint4 *>(gw + off));
+    o.cu[i] = load_stream16(reinterpret_cast<const uint4 *>(uw + off));
   }
+  o.ok = ok;
+}
+
+// Gate/up rows 2t, 2t+1 of a fix-up expert from its loaded operands, with the
+// lane partition and summation order of WideU::run; published as one flagged
+// entry of the expert's activations.
+template <class C>
+__device__ __forceinline__ void wide_fix_compute(int lane, int t, const WideFix<C> &o,
+                                                 const uint4 *act_l, const float *asum_l,
+                                                 uint64_t *hf, uint32_t fl) {
+  constexpr int U = C::U, SGU = C::SGU, CPLU = C::CPLU;
+  const int uj = lane % SGU;
   float pg = 0.f, pu = 0.f;
 #pragma unroll
   for (int i = 0; i < CPLU; ++i) {
@@ -474,20 +493,20 @@ __device__ __forceinline__ void wide_fix_task(int lane, const StackArgs &a, int3
 #pragma unroll
       for (int q = 0; q < 4; ++q) xa[q] = act_l[q * U + c];
       const float xs = asum_l[c];
-      const float Sg = bf16_to_f32(sv[0][i]), Bg = bf16_to_f32(sv[1][i]);
-      const float Su = bf16_to_f32(sv[2][i]), Bu = bf16_to_f32(sv[3][i]);
-      pg += Sg * chunk_dot_regs(cg[i], xa) + (Bg - 128.f * Sg) * xs;
-      pu += Su * chunk_dot_regs(cu[i], xa) + (Bu - 128.f * Su) * xs;
+      const float Sg = bf16_to_f32(o.sv[0][i]), Bg = bf16_to_f32(o.sv[1][i]);
+      const float Su = bf16_to_f32(o.sv[2][i]), Bu = bf16_to_f32(o.sv[3][i]);
+      pg += Sg * chunk_dot_regs(o.cg[i], xa) + (Bg - 128.f * Sg) * xs;
+      pu += Su * chunk_dot_regs(o.cu[i], xa) + (Bu - 128.f * Su) * xs;
     }
   }
   float g = group_sum<SGU>(pg);
   float u = group_sum<SGU>(pu);
   if (C::PBIAS_) {
-    g += gbv;
-    u += ubv;
+    g += o.gbv;
+    u += o.ubv;
   }
   uint32_t hb = 0;
-  if (ok) hb = f32_to_bf16(wide_act<C>(g, u));
+  if (o.ok) hb = f32_to_bf16(wide_act<C>(g, u));
   else if (lane == 0) flag_error();
   static_assert(C::RPSU == 2, "two rows per task");
   const uint32_t h0 = __builtin_amdgcn_readlane(hb, 0), h1 = __builtin_amdgcn_readlane(hb, 32);
@@ -738,11 +757,23 @@ __global__ __launch_bounds__(512) void stack_wide_kernel(StackArgs a) {
       // waves like the others)
       {
         constexpr int FT = F / 2;
+        constexpr int STRIDE = C::WAVES_U * NWG;
         const int nf = n_fix;
-        for (int t = wave * NWG + wg; t < nf * FT; t += C::WAVES_U * NWG) {
-          const int p = fix_pos[t / FT];
-          wide_fix_task<C>(lane, a, sel_ref[pos_rank[p]], t % FT, act_l, asum_l,
-                           hfix + (size_t)p * (F / 2), fl);
+        // two tasks at a time: the second one's loads in flight while the
+        // first one computes
+        for (int t = wave * NWG + wg; t < nf * FT; t += 2 * STRIDE) {
+          const int p0 = fix_pos[t / FT], t2 = t + STRIDE;
+          WideFix<C> f0;
+          wide_fix_load<C>(lane, a, sel_ref[pos_rank[p0]], t % FT, f0);
+          if (t2 < nf * FT) {
+            const int p1 = fix_pos[t2 / FT];
+            WideFix<C> f1;
+            wide_fix_load<C>(lane, a, sel_ref[pos_rank[p1]], t2 % FT, f1);
+            wide_fix_compute<C>(lane, t % FT, f0, act_l, asum_l, hfix + (size_t)p0 * FT, fl);
+            wide_fix_compute<C>(lane, t2 % FT, f1, act_l, asum_l, hfix + (size_t)p1 * FT, fl);
+          } else {
+            wide_fix_compute<C>(lane, t % FT, f0, act_l, asum_l, hfix + (size_t)p0 * FT, fl);
+          }
         }
       }
       if (wave == 0) trace_mark(a, l, TR_FIXED);
