@@ -10,21 +10,27 @@
 // The lookahead router predicts layer l+1's experts during layer l
 // (engine_v3.py:509-527).  Here that prediction stages the expert bytes:
 // at the end of layer l every workgroup issues the register loads of the
-// gate/up and down codes it will need in layer l+1 if the prediction is
-// right, so the reads overlap the wait for the layer boundary.  Per layer:
+// gate/up codes it will need in layer l+1 if the prediction is right, so
+// the reads overlap the wait for the layer boundary; the down codes follow
+// inside layer l+1, each wave's once its earlier work there is done (issued
+// at layer l's end they would queue ahead of the boundary poll).  Per layer:
 //
 //   wait   : layer l-1 complete (its output is this layer's input)
-//   split  : waves 0-5 gate/up + activation for the PREDICTED expert at this
-//            workgroup's position (24 rows), and waves 0-1 one 4-row task of
+//   split  : (expert position p = rank p of the prediction lives on XCD p:
+//            the workgroups w with w % 8 == p) waves 0-5 gate/up + activation
+//            for the PREDICTED expert at this workgroup's position (24 rows,
+//            published XCD-locally), and waves 0-1 one 4-row task of
 //            the two SPARE positions (lookahead ranks K, K+1; their bytes go
 //            to LDS by direct-to-LDS loads while the predicted rows compute);
 //            wave 6 one router row (+ the lookahead row), then the lookahead
 //            ranking of layer l+1; wave 7 waits for all router rows and ranks
 //            them (every workgroup redundantly, identically)
 //   fix-up : routed experts that were not predicted get gate/up now
-//   D      : down + score-weighted combine over the k routed experts, 8
-//            output rows per workgroup, wave = expert; then the staging
-//            loads of layer l+1
+//   D      : the down rows (64 per workgroup, 8 per wave) of the routed
+//            expert at the workgroup's position, its activations polled from
+//            the XCD's L2; the score-weighted rows go out as that routing
+//            rank's partial output, which the next layer combines in rank
+//            order; then the gate/up staging loads of layer l+1
 //
 // Activations and the combine are indexed by routing rank, so results are
 // bit-identical to route_kernel + ffn_decode whatever was predicted.
@@ -871,6 +877,10 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
                      layer_flag(a, l));
       if (spare)
         put_acts(hpred + (size_t)(K + ts / FT) * (F / 2) + 2 * (ts % FT), hs, layer_flag(a, l));
+      // this wave's down rows of the position's predicted expert, issued once
+      // its gate/up work is done (at the previous layer's end they would
+      // queue ahead of the boundary poll)
+      if (upos < pcnt) d_load<C>(a, pred_ref[l & 1][upos], dwrow, cd, sdr);
       // layer l-1's score-weighted outputs of this workgroup's rows, complete
       // since this layer's start: loaded now, summed before the arrival
       if (wave == W_COMB && l > 0)
@@ -1158,13 +1168,13 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
     wg_arrive(counter<WS>(a, l, CNT_D));
     if (wave == 0) trace_mark(a, l, TR_D_ARRIVED);
     // ----------------------------- staging loads of layer l+1's prediction
-    // (the ranking wave's down rows are staged after the next layer's wait,
-    // the router wave's after its router row)
+    // (its down rows are staged during layer l+1: the ranking wave's after
+    // the boundary, the router wave's after its router row, the gate/up
+    // waves' after their gate/up rows)
     if (has_next) {
       const int pc = pred_cnt[(l + 1) & 1];
       const int32_t *Rn = pred_ref[(l + 1) & 1];
       if (upos < pc) u_load<C>(a, Rn[upos], urow0, cg, cu, sr);
-      if (wave != W_RANK && wave != W_ROUTER && upos < pc) d_load<C>(a, Rn[upos], dwrow, cd, sdr);
     }
   }
   // the last layer's outputs: its partials are complete once every
