@@ -639,27 +639,37 @@ __device__ __forceinline__ void get_acts(const uint64_t *hf, uint32_t fl, const 
 // PPW takes piece PPW * w + j), polled until each carries the flag `fl`.
 // Lanes past PPW load the wave's first piece and do not wait on it.
 template <int PPW>
-__device__ __forceinline__ uint4 get_acts_part(const uint64_t *hf, int w, uint32_t fl,
-                                               const Abort &ab) {
+__device__ __forceinline__ void acts_part_issue(const uint64_t *hf, int w, uint64_t (&v)[4]) {
   const int lane = threadIdx.x & 63;
-  const bool mine = lane < PPW;
-  const uint64_t *e = hf + 4 * (PPW * w + (mine ? lane : 0));
-  uint32_t spins = 0;
-  uint4 p;
-  while (true) {
-    uint64_t v[4];
+  const uint64_t *e = hf + 4 * (PPW * w + (lane < PPW ? lane : 0));
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      v[q] = __hip_atomic_load(e + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int q = 0; q < 4; ++q)
+    v[q] = __hip_atomic_load(e + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// get_acts_part from a first round already issued (acts_part_issue, into v):
+// its flags checked, further rounds polled as needed.
+template <int PPW>
+__device__ __forceinline__ uint4 acts_part_finish(const uint64_t *hf, int w, uint32_t fl,
+                                                  const Abort &ab, uint64_t (&v)[4]) {
+  const bool mine = (threadIdx.x & 63) < PPW;
+  uint32_t spins = 0;
+  while (true) {
     bool ok = true;
 #pragma unroll
     for (int q = 0; q < 4; ++q) ok = ok && (uint32_t)(v[q] >> 32) == fl;
-    p = make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
     if (__ballot(mine && !ok) == 0) break;
     if (ab.gave_up(++spins)) break;
     __builtin_amdgcn_s_sleep(1);
+    acts_part_issue<PPW>(hf, w, v);
   }
-  return p;
+  return make_uint4((uint32_t)v[0], (uint32_t)v[1], (uint32_t)v[2], (uint32_t)v[3]);
+}
+template <int PPW>
+__device__ __forceinline__ uint4 get_acts_part(const uint64_t *hf, int w, uint32_t fl,
+                                               const Abort &ab) {
+  uint64_t v[4];
+  acts_part_issue<PPW>(hf, w, v);
+  return acts_part_finish<PPW>(hf, w, fl, ab, v);
 }
 
 // Register loads of one workgroup's gate/up block (waves 0..WAVES_U-1: the
@@ -1088,6 +1098,11 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
       if (lane == 0) n_miss = __popcll(tm);
     }
     lds_barrier();   // the routing's results (LDS) for every wave
+    // the first poll of the position's predicted activations, issued before
+    // this phase's LDS and scalar reads: the down rows use it if the routing
+    // kept that expert
+    uint64_t pv4[4] = {0, 0, 0, 0};
+    if (upos < pcnt) acts_part_issue<PPW>(hpred + (size_t)upos * (F / 2), wave, pv4);
     if (wave == 0) trace_mark(a, l, TR_SELECTED);
     if (tid == 0) {   // next layer's slots; nobody touches them before its start
       staged[(l + 1) & 1] = 0;
@@ -1135,7 +1150,8 @@ __global__ __launch_bounds__(512) void stack_decode_kernel(StackArgs a) {
         const uint64_t *hf = fx < 0    ? hpred + (size_t)upos * (F / 2)
                              : src >= 0 ? hfix + (size_t)src * (F / 2)
                                         : hpred + (size_t)(K - 1 - src) * (F / 2);
-        const uint4 pc = get_acts_part<PPW>(hf, wave, layer_flag(a, l), ab);
+        const uint4 pc = fx < 0 ? acts_part_finish<PPW>(hf, wave, layer_flag(a, l), ab, pv4)
+                                : get_acts_part<PPW>(hf, wave, layer_flag(a, l), ab);
         if (wave == 0) trace_mark(a, l, TR_D_WAITED);
         const int i = PPW * wave + lane;
         float s = 0.f;
