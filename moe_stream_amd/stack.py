@@ -44,14 +44,17 @@ def routers(geom: Geometry, n_layers: int, device, seed: int, zipf_s: float | No
 class DecodeStack:
     def __init__(self, geom: Geometry, n_layers: int, n_slots: int, device="cuda",
                  seed: int = synth.SEED_BASE + 2, zipf_s: float | None = 1.1,
-                 router_bias: bool = False, widen: int = 1, resident=None):
+                 router_bias: bool = False, widen: int = 1, resident=None,
+                 k_pred: int | None = None):
         self.geom = geom
         self.L = n_layers
         self.E = geom.n_experts
         self.k = geom.top_k
         self.device = _norm_device(device)
         self.widen = widen
-        self.k_pred = min(self.k * widen, self.E)
+        # the lookahead width: k x widen (PF_WIDEN, engine_v3.py:84), or any
+        # width the C ABI accepts (1..min(E, 64)), narrower than k included
+        self.k_pred = min(self.k * widen, self.E) if k_pred is None else int(k_pred)
         n_rec = n_layers * self.E
         self.store = synth.make_store(geom, n_rec, self.device, seed)
         self.pool = SlotPool(geom, n_slots, self.device, store=self.store)

@@ -65,6 +65,30 @@ def test_persistent_wide_lookahead_equals_per_layer():
     torch.cuda.empty_cache()
 
 
+def test_persistent_narrow_lookahead_equals_per_layer():
+    """k_pred = 4 (half of top-k): only positions 0-3 of each layer have a
+    predicted expert staged, so the routed experts of the other positions all
+    go through the spare positions (lookahead ranks 8 and 9, still ranked) or
+    the fix-up pass; every output equals the per-layer launches'."""
+    st = DecodeStack(G.QWEN3_30B_A3B, 4, 256, "cuda", seed=20260613, zipf_s=1.1, k_pred=4)
+    assert st.k_pred == 4
+    xs = synth.hidden_states(3, st.L, 2048, "cuda", 20260614)
+    for t in range(xs.shape[0]):
+        st.run_token(xs[t], use_graph=False)
+        ids, sc, refs, pred = st.routed()
+        y_ref = st.y.clone()
+        st.token_persistent(xs[t])
+        torch.cuda.synchronize()
+        ops.check_device_error()
+        np.testing.assert_array_equal(st.p_ids.cpu().numpy(), ids)
+        np.testing.assert_array_equal(st.p_scores.cpu().numpy(), sc)
+        np.testing.assert_array_equal(st.p_refs.cpu().numpy(), refs)
+        np.testing.assert_array_equal(st.p_pred.cpu().numpy()[:-1], pred[:-1])
+        assert torch.equal(st.p_y, y_ref), t
+    del st
+    torch.cuda.empty_cache()
+
+
 def test_graph_replays_equal_eager(stack):
     """The per-layer launches captured once as a HIP graph and replayed for
     several tokens, with eager work of the same stack between the replays:
