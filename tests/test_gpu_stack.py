@@ -89,6 +89,33 @@ def test_persistent_narrow_lookahead_equals_per_layer():
     torch.cuda.empty_cache()
 
 
+def test_persistent_unbiased_router_many_misses_equals_per_layer():
+    """No router bias and layer inputs far apart (each layer's input adds
+    noise ten times its own scale): the lookahead on the previous layer's
+    input then predicts few of the routed experts, so most of each layer's 8
+    go through the spare positions or the fix-up slots (up to all 8 at once);
+    every output still equals the per-layer launches'."""
+    st = DecodeStack(G.QWEN3_30B_A3B, 4, 256, "cuda", seed=20260615, zipf_s=None)
+    xs = synth.hidden_states(3, st.L, 2048, "cuda", 20260616, step=10.0)
+    unstaged = 0
+    for t in range(xs.shape[0]):
+        st.run_token(xs[t], use_graph=False)
+        ids, sc, refs, pred = st.routed()
+        y_ref = st.y.clone()
+        st.token_persistent(xs[t])
+        torch.cuda.synchronize()
+        ops.check_device_error()
+        np.testing.assert_array_equal(st.p_ids.cpu().numpy(), ids)
+        np.testing.assert_array_equal(st.p_scores.cpu().numpy(), sc)
+        np.testing.assert_array_equal(st.p_refs.cpu().numpy(), refs)
+        np.testing.assert_array_equal(st.p_pred.cpu().numpy()[:-1], pred[:-1])
+        assert torch.equal(st.p_y, y_ref), t
+        unstaged += sum(len(set(ids[l]) - set(pred[l - 1])) for l in range(1, st.L))
+    assert unstaged >= 3 * (st.L - 1) * 4   # on average half of the routed experts or more
+    del st
+    torch.cuda.empty_cache()
+
+
 def test_graph_replays_equal_eager(stack):
     """The per-layer launches captured once as a HIP graph and replayed for
     several tokens, with eager work of the same stack between the replays:
@@ -162,3 +189,27 @@ def test_gptoss_persistent_equals_per_layer(gptoss_stack, ordinary):
         np.testing.assert_array_equal(st.p_refs.cpu().numpy(), refs)
         np.testing.assert_array_equal(st.p_pred.cpu().numpy()[:-1], pred[:-1])
         assert torch.equal(st.p_y, y_ref), t
+
+
+@pytest.mark.parametrize("ordinary", [False, True])
+def test_gptoss_persistent_many_misses_equals_per_layer(gptoss_stack, ordinary):
+    """The wide whole-token kernel with layer inputs far apart (noise ten
+    times the input's scale added per layer): the lookahead misses most of
+    the 4 routed experts, so most positions take a fix-up expert; routing,
+    lookahead and outputs still equal the per-layer launches' bit for bit."""
+    st = gptoss_stack
+    xs = synth.hidden_states(3, st.L, 2880, "cuda", 20260631 + int(ordinary), step=10.0)
+    unstaged = 0
+    for t in range(xs.shape[0]):
+        st.run_token(xs[t], use_graph=False)
+        ids, sc, refs, pred = st.routed()
+        y_ref = st.y.clone()
+        st.token_persistent(xs[t], ordinary=ordinary)
+        st.check_persistent()
+        np.testing.assert_array_equal(st.p_ids.cpu().numpy(), ids)
+        np.testing.assert_array_equal(st.p_scores.cpu().numpy(), sc)
+        np.testing.assert_array_equal(st.p_refs.cpu().numpy(), refs)
+        np.testing.assert_array_equal(st.p_pred.cpu().numpy()[:-1], pred[:-1])
+        assert torch.equal(st.p_y, y_ref), t
+        unstaged += sum(len(set(ids[l]) - set(pred[l - 1][:st.k])) for l in range(1, st.L))
+    assert unstaged >= 3 * (st.L - 1) * 2   # on average half of the routed experts or more
