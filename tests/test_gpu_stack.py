@@ -213,3 +213,28 @@ def test_gptoss_persistent_many_misses_equals_per_layer(gptoss_stack, ordinary):
         assert torch.equal(st.p_y, y_ref), t
         unstaged += sum(len(set(ids[l]) - set(pred[l - 1][:st.k])) for l in range(1, st.L))
     assert unstaged >= 3 * (st.L - 1) * 2   # on average half of the routed experts or more
+
+
+@pytest.mark.parametrize("k_pred", [2, 8])
+def test_gptoss_persistent_lookahead_width_equals_per_layer(k_pred):
+    """The wide whole-token kernel with a lookahead narrower (2: positions 2
+    and 3 have no staged expert) and wider (8: ranks past top-4 predicted but
+    not staged) than top-4: routing, lookahead and outputs equal the
+    per-layer launches' bit for bit."""
+    st = DecodeStack(G.GPT_OSS_120B, 4, 240, "cuda", seed=20260641, zipf_s=None,
+                     router_bias=True, k_pred=k_pred)
+    assert st.k_pred == k_pred and st.persistent_supported()
+    xs = synth.hidden_states(3, st.L, 2880, "cuda", 20260642 + k_pred)
+    for t in range(xs.shape[0]):
+        st.run_token(xs[t], use_graph=False)
+        ids, sc, refs, pred = st.routed()
+        y_ref = st.y.clone()
+        st.token_persistent(xs[t])
+        st.check_persistent()
+        np.testing.assert_array_equal(st.p_ids.cpu().numpy(), ids)
+        np.testing.assert_array_equal(st.p_scores.cpu().numpy(), sc)
+        np.testing.assert_array_equal(st.p_refs.cpu().numpy(), refs)
+        np.testing.assert_array_equal(st.p_pred.cpu().numpy()[:-1], pred[:-1])
+        assert torch.equal(st.p_y, y_ref), t
+    del st
+    torch.cuda.empty_cache()
