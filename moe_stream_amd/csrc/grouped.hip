@@ -838,7 +838,10 @@ static void launch_gd(dim3 g, hipStream_t s, const PoolArgs &pa, const uint16_t 
                      pa, hq, rsh, 1, perm, tiles, nt, nullptr, nullptr, sc, yp, 0, 0.f, 0.f);
 }
 
-// (features per work item, waves) of gate/up and of down per geometry
+// (features per work item, waves) of gate/up and of down per geometry.  Only
+// these shapes are validated (the grouped parity tests, the 512-token one
+// included); others that compile are not all correct: gate/up (32, 2)
+// computes wrong rows, down (64, 4) wrong outputs at 64-row tiles.
 #define MOE_GROUPED_GEOM(D, F, PB, NBU, WU, NBD, WD)                                     \
   {D, F, PB, NBU, NBD, &launch_gg<D, F, PB, NBU, WU>, &launch_gd<D, F, PB, NBD, WD>}
 static const GroupedLaunch kGroupedTable[] = {
