@@ -667,6 +667,10 @@ __device__ __forceinline__ void grouped_item(
   constexpr bool FUSE = GU && NB % 64 == 0;
   constexpr int OB = GU ? 2 : 4;                          // output bytes per element
   constexpr bool STAGE = ROWS * NB * OB <= (int)(4 * kTileM * 8 * sizeof(uint4));
+  // the staged tile's element swizzle: XOR with 16 x ((row >> 2) & mask), the
+  // mask kept so that an element never leaves its row (NB features)
+  constexpr int SWM = NB % 64 == 0 ? 3 : NB % 32 == 0 ? 1 : 0;
+  auto swz = [](int r) { return ((r >> 2) & SWM) << 4; };
   __syncthreads();
   char *tile = reinterpret_cast<char *>(L.a[0]);
 #pragma unroll
@@ -688,9 +692,9 @@ __device__ __forceinline__ void grouped_item(
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int rr = rb * 16 + 4 * kq + e;   // (uniform over each 16-lane row)
-        // staged tile: row rr, element npl ^ (16 * ((rr >> 2) & 3)) (the 4
-        // rows of one store fall on distinct banks)
-        const int ec = npl ^ (((rr >> 2) & 3) << 4);
+        // staged tile: row rr, element npl ^ swz(rr) (the 4 rows of one
+        // store fall on distinct banks)
+        const int ec = npl ^ swz(rr);
         if (GU) {
           const float hv = apply_act(act, acc[rb][cb][0][e] + pb[0],
                                      acc[rb][cb][NPROJ - 1][e] + pb[NPROJ - 1], alpha, limit);
@@ -727,7 +731,7 @@ __device__ __forceinline__ void grouped_item(
     for (int it = 0; it < (ROWS * CPR + NT - 1) / NT; ++it) {
       const int i = tid_e + NT * it, r = i / CPR, c = i % CPR;
       if (i < ROWS * CPR && r < rows) {
-        const int ec = (c * EPC) ^ (((r >> 2) & 3) << 4);
+        const int ec = (c * EPC) ^ swz(r);
         const uint4 v = *reinterpret_cast<const uint4 *>(tile + (r * NB + ec) * OB);
         if (GU)
           *reinterpret_cast<uint4 *>(h_out + (int64_t)(r0 + r) * F + nb0 + c * EPC) = v;
@@ -839,9 +843,9 @@ static void launch_gd(dim3 g, hipStream_t s, const PoolArgs &pa, const uint16_t 
 }
 
 // (features per work item, waves) of gate/up and of down per geometry.  Only
-// these shapes are validated (the grouped parity tests, the 512-token one
-// included); others that compile are not all correct: gate/up (32, 2)
-// computes wrong rows, down (64, 4) wrong outputs at 64-row tiles.
+// these shapes are validated (the grouped parity tests with tiles of 1 to 64
+// rows); another shape that compiles is not known to be correct (down at
+// (64, 4) was measured wrong at 64-row tiles).
 #define MOE_GROUPED_GEOM(D, F, PB, NBU, WU, NBD, WD)                                     \
   {D, F, PB, NBU, NBD, &launch_gg<D, F, PB, NBU, WU>, &launch_gd<D, F, PB, NBD, WD>}
 static const GroupedLaunch kGroupedTable[] = {

@@ -162,6 +162,38 @@ def test_grouped_gptoss_matches_oracle():
     torch.cuda.empty_cache()
 
 
+def test_grouped_gptoss_full_tiles_match_oracle():
+    """gpt-oss geometry with 64-row tiles: 160 tokens all routed to experts
+    0 and 1 (plus two others each), so those two slots hold 160 rows each
+    (tiles of 64, 64 and 32 rows) and every row-block count of both kernels
+    runs; the first tokens' rows lie in full tiles."""
+    layer = Layer(G.GPT_OSS_120B, 136, seed=20260051, router_bias=True)
+    g = layer.geom
+    T = 160
+    rng = np.random.default_rng(20260052)
+    ids = np.zeros((T, g.top_k), dtype=np.int64)
+    for t in range(T):
+        ids[t] = [0, 1] + list(rng.choice(np.arange(2, g.n_experts), g.top_k - 2, replace=False))
+    sc = rng.random((T, g.top_k)).astype(np.float32)
+    sc = (sc / sc.sum(axis=1, keepdims=True)).astype(np.float32)
+    refs = layer.table[torch.tensor(ids, device="cuda")].to(torch.int32).contiguous()
+    scores = torch.tensor(sc, device="cuda")
+    x = bf16_randn((T, g.d_model), seed=20260053)
+    out32 = torch.zeros((T, g.d_model), dtype=torch.float32, device="cuda")
+    ops.ffn_grouped(layer.pool, refs, scores, x, out_f32=out32)
+    torch.cuda.synchronize()
+    ops.check_device_error()
+    n = 12
+    y64 = N.moe_block_batch(bf16_values(x)[:n], ids[:n], sc[:n].astype(np.float64),
+                            layer.expert, "gptoss", "f64", g.alpha, g.limit)
+    o32 = out32.cpu().numpy()
+    e64 = max(N.rel_err(o32[t], y64[t]) for t in range(n))
+    print(f"gpt-oss grouped, 64-row tiles: worst-token rel err vs f64 {e64:.2e}")
+    assert e64 < TOL, e64
+    del layer
+    torch.cuda.empty_cache()
+
+
 def test_grouped_full_size_equals_decode(qwen_layer):
     """512 tokens x top-8 with Zipf skew (4096 pairs): the grouped MFMA block
     matches the fp64 oracle on every token, and the decode kernels on the
