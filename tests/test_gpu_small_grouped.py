@@ -139,3 +139,18 @@ def test_out_of_range_ref_in_a_group(qwen_layer):
         ops.check_device_error()
     torch.cuda.synchronize()
     assert torch.equal(y, o)
+
+
+@pytest.mark.parametrize("geo", ["qwen3", "gptoss"])
+def test_every_token_on_the_same_experts_at_the_limit(qwen_layer, gptoss_layer, geo):
+    """Maximal sharing at the small-T kernels' limit (T x k = 256 pairs):
+    every token routed to the same experts, so each slot serves T pairs
+    (32 for Qwen3, 64 for gpt-oss); outputs equal one call per token."""
+    layer = qwen_layer if geo == "qwen3" else gptoss_layer
+    g = layer.geom
+    T = 256 // g.top_k
+    rng = np.random.default_rng(9 + g.top_k)
+    ids = np.tile(rng.permutation(g.n_experts)[:g.top_k], (T, 1))
+    sc = rng.dirichlet(np.ones(g.top_k), T).astype(np.float32)
+    x = bf16_randn((T, g.d_model), seed=20260960 + g.top_k)
+    _grouped_vs_per_token(layer, ids, sc, x)
