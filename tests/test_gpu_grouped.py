@@ -76,6 +76,30 @@ def test_route_many_tokens_matches_oracle(qwen_layer):
     assert int(bufs.miss.item()) == 0
 
 
+def test_route_many_tokens_gptoss_matches_oracle():
+    """gpt-oss routing on the MFMA router: top-4 of the raw biased logits
+    over d_model 2880, 100 tokens (a ragged last 16-token tile), with a
+    biased lookahead router ranking the top 8 of the next layer."""
+    layer = Layer(G.GPT_OSS_120B, 136, seed=20260054, router_bias=True)
+    g = layer.geom
+    T = 100
+    x = bf16_randn((T, g.d_model), seed=20260055)
+    Wn, bn = synth.router_weights(g, 1, "cuda", 20260056, with_bias=True)
+    Wn, bn = Wn[0].contiguous(), bn[0].contiguous()
+    bufs = ops.route(x, layer.W, layer.bias, g.routing, g.norm_topk_prob, g.top_k,
+                     W_next=Wn, bias_next=bn, k_pred=8, table=layer.table)
+    torch.cuda.synchronize()
+    ids, sc, exact = _check_ids(layer, x, bufs)
+    assert exact >= 0.9 * T
+    Zn = N.router_logits(bf16_values(x), bf16_bits(Wn), bf16_bits(bn), "mlx")
+    pred = bufs.pred.cpu().numpy()
+    for t in range(T):
+        assert N.ids_match(Zn[t], N.top_k_indices(Zn[t], 8), pred[t]), t
+    assert int(bufs.miss.item()) == 0
+    del layer
+    torch.cuda.empty_cache()
+
+
 def test_route_many_equals_fused_small_T(qwen_layer):
     """The MFMA router (T > 16) and the fused router (T <= 16) select the
     same experts for the same tokens (their fp32 logits differ only in
