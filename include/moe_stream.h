@@ -260,8 +260,10 @@ int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_lay
 /*
  * Device-side (layer, expert) -> slot lookup for n ids (the index build of
  * engine_v3.py:550-552 against the slot table of engine_v3.py:215):
- * slot_refs[i] = table[ids[i]] for ids in [0, E); out-of-range ids give
- * MOE_ERR_DEVICE through the flag in *miss_count's sibling error word.
+ * slot_refs[i] = table[ids[i]] for ids in [0, E); *miss_count (if not NULL)
+ * is incremented by the number of refs < 0.  An id outside [0, E) gives
+ * ref 0 and raises the device error flag that moe_check_device_error
+ * reports as MOE_ERR_DEVICE.
  */
 int moe_slot_lookup(const int32_t *table, int32_t E, const int32_t *ids,
                     int32_t n, int32_t *slot_refs, int32_t *miss_count,

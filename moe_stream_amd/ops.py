@@ -60,6 +60,76 @@ def ffn_decode(pool, slot_refs: torch.Tensor, scores: torch.Tensor,
                 scores, x, out, out_f32, stream, workspace)
 
 
+def ffn_decode_up(pool, slot_refs: torch.Tensor, x: torch.Tensor,
+                  workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """First half of ffn_decode: the gate/up projections and activation of
+    every (token, expert) pair into the workspace, which is returned for
+    ffn_decode_down (pass the same tensor; it is not shared with ffn_decode's
+    cached workspace)."""
+    geom: Geometry = pool.geom
+    x = x.view(1, -1) if x.dim() == 1 else x
+    T, D = x.shape
+    if D != geom.d_model:
+        raise ValueError(f"x has {D} features, geometry {geom.d_model}")
+    k = slot_refs.numel() // T
+    _req(x, torch.bfloat16, "x", device=pool.device)
+    _req(slot_refs, torch.int32, "slot_refs", T * k, pool.device)
+    g = geom.c_geom()
+    L = _lib.lib()
+    need = L.moe_ffn_decode_workspace(C.byref(g), T, k)
+    if need == 0:
+        raise ValueError(f"moe_ffn_decode_up: unsupported T={T}, k={k}")
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    _lib.check(L.moe_ffn_decode_up(
+        C.byref(pool.c_view()), C.byref(g), _p(slot_refs), _p(x), T, k,
+        _p(workspace), workspace.numel(), _lib.stream_ptr(stream)))
+    return workspace
+
+
+def ffn_decode_down(pool, slot_refs: torch.Tensor, scores: torch.Tensor,
+                    workspace: torch.Tensor, out: torch.Tensor | None = None,
+                    out_f32: torch.Tensor | None = None, stream=None):
+    """Second half of ffn_decode: the down projections of the activations
+    ffn_decode_up left in `workspace`, weighted by scores and summed per
+    token.  slot_refs int32 [T, k] and scores fp32 [T, k] as for ffn_decode."""
+    geom: Geometry = pool.geom
+    T, k = slot_refs.shape
+    D = geom.d_model
+    _req(slot_refs, torch.int32, "slot_refs", T * k, pool.device)
+    _req(scores, torch.float32, "scores", T * k, pool.device)
+    _req(workspace, torch.uint8, "workspace", device=pool.device)
+    if out is None and out_f32 is None:
+        out = torch.empty((T, D), dtype=torch.bfloat16, device=slot_refs.device)
+    if out is not None:
+        _req(out, torch.bfloat16, "out", T * D, pool.device)
+    if out_f32 is not None:
+        _req(out_f32, torch.float32, "out_f32", T * D, pool.device)
+    g = geom.c_geom()
+    _lib.check(_lib.lib().moe_ffn_decode_down(
+        C.byref(pool.c_view()), C.byref(g), _p(slot_refs), _p(scores), T, k,
+        _p(out), _p(out_f32), _p(workspace), workspace.numel(),
+        _lib.stream_ptr(stream)))
+    return out if out is not None else out_f32
+
+
+def slot_lookup(table: torch.Tensor, ids: torch.Tensor,
+                miss: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """slot_refs = table[ids] on device (engine_v3.py:550-552).  table int32
+    [E]; ids int32 of any shape.  miss (int32 [1], optional) is incremented
+    by the number of refs < 0; an id outside [0, E) gives ref 0 and raises
+    the device error flag that check_device_error reports."""
+    _req(table, torch.int32, "table")
+    _req(ids, torch.int32, "ids", device=table.device)
+    if miss is not None:
+        _req(miss, torch.int32, "miss", 1, table.device)
+    refs = torch.empty_like(ids)
+    _lib.check(_lib.lib().moe_slot_lookup(
+        _p(table), table.numel(), _p(ids), ids.numel(), _p(refs), _p(miss),
+        _lib.stream_ptr(stream)))
+    return refs
+
+
 def ffn_grouped(pool, slot_refs: torch.Tensor, scores: torch.Tensor,
                 x: torch.Tensor, out: torch.Tensor | None = None,
                 out_f32: torch.Tensor | None = None, stream=None,

@@ -139,3 +139,75 @@ def test_out_of_range_ref_is_reported_not_faulting(qwen_layer):
         ops.check_device_error()
     assert ei.value.code == _lib.MOE_ERR_DEVICE
     ops.check_device_error()   # cleared
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_split_halves_equal_one_call(qwen_layer, T):
+    """moe_ffn_decode_up then moe_ffn_decode_down, each its own call (the
+    second on another stream that waits for the first), give the bytes of
+    moe_ffn_decode; T=3 takes the kernels that group pairs per expert."""
+    g = qwen_layer.geom
+    x = bf16_randn((T, 2048), seed=20260030 + T)
+    bufs = ops.route(x, qwen_layer.W, None, g.routing, g.norm_topk_prob, g.top_k,
+                     table=qwen_layer.table)
+    ref32 = torch.zeros((T, 2048), dtype=torch.float32, device="cuda")
+    ref = torch.zeros((T, 2048), dtype=torch.bfloat16, device="cuda")
+    ops.ffn_decode(qwen_layer.pool, bufs.slot_refs, bufs.scores, x, out=ref, out_f32=ref32)
+    ws = ops.ffn_decode_up(qwen_layer.pool, bufs.slot_refs, x)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    out32 = torch.zeros((T, 2048), dtype=torch.float32, device="cuda")
+    with torch.cuda.stream(side):
+        out = ops.ffn_decode_down(qwen_layer.pool, bufs.slot_refs, bufs.scores, ws,
+                                  out_f32=out32, stream=side)
+    torch.cuda.synchronize()
+    ops.check_device_error()
+    assert out is out32
+    assert torch.equal(out32, ref32)
+    out_b = ops.ffn_decode_down(qwen_layer.pool, bufs.slot_refs, bufs.scores, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(out_b, ref)
+    with pytest.raises(_lib.MoeError):   # a workspace too small for T x k
+        ops.ffn_decode_down(qwen_layer.pool, bufs.slot_refs, bufs.scores, ws[:256])
+
+
+def test_split_halves_gptoss():
+    layer = Layer(G.GPT_OSS_120B, 136, seed=20260033, router_bias=True)
+    g = layer.geom
+    x = bf16_randn((1, g.d_model), seed=20260034)
+    bufs = ops.route(x, layer.W, layer.bias, g.routing, g.norm_topk_prob, g.top_k,
+                     table=layer.table)
+    ref = ops.ffn_decode(layer.pool, bufs.slot_refs, bufs.scores, x)
+    ws = ops.ffn_decode_up(layer.pool, bufs.slot_refs, x)
+    out = ops.ffn_decode_down(layer.pool, bufs.slot_refs, bufs.scores, ws)
+    torch.cuda.synchronize()
+    ops.check_device_error()
+    assert torch.equal(out, ref)
+    del layer
+    torch.cuda.empty_cache()
+
+
+def test_slot_lookup(qwen_layer):
+    """slot_refs = table[ids] for ids of any count (several 256-thread
+    blocks and a ragged last one); refs < 0 (experts not resident) are
+    counted into miss; an id outside [0, E) is reported, not read."""
+    rng = np.random.default_rng(20260035)
+    table = qwen_layer.perm.astype(np.int32).copy()
+    table[rng.choice(128, 10, replace=False)] = -1
+    t_dev = torch.tensor(table, device="cuda")
+    for n in (1, 300, 4096 + 7):
+        ids = rng.integers(0, 128, n).astype(np.int32)
+        miss = torch.zeros(1, dtype=torch.int32, device="cuda")
+        refs = ops.slot_lookup(t_dev, torch.tensor(ids, device="cuda"), miss)
+        torch.cuda.synchronize()
+        ops.check_device_error()
+        np.testing.assert_array_equal(refs.cpu().numpy(), table[ids])
+        assert int(miss.item()) == int((table[ids] < 0).sum())
+    ids = torch.tensor([3, 128, 5], dtype=torch.int32, device="cuda")
+    refs = ops.slot_lookup(t_dev, ids)
+    torch.cuda.synchronize()
+    with pytest.raises(_lib.MoeError) as ei:
+        ops.check_device_error()
+    assert ei.value.code == _lib.MOE_ERR_DEVICE
+    ops.check_device_error()   # cleared
+    assert refs.cpu().tolist() == [table[3], 0, table[5]]
