@@ -246,8 +246,11 @@ enum {
 size_t moe_stack_workspace(const moe_geom *g, int32_t n_layers, int32_t E, int32_t k);
 /* Phase trace of moe_stack_decode: while set, each launch writes wall-clock
  * stamps (wall_clock64 ticks, 100 MHz) of every workgroup (up to 256) at the
- * 12 phase points of every layer into device_buf ([256][n_layers][12]
- * uint64).  NULL turns it off.  Process-wide setting. */
+ * 15 phase points of every layer into device_buf ([256][n_layers][15]
+ * uint64; point 0 = layer start, 6 = the workgroup's down rows published;
+ * a point a workgroup does not reach keeps its old value).  A launch with a
+ * buffer smaller than that fails with MOE_ERR_INVALID.  NULL turns it off.
+ * Process-wide setting; outputs are the same with and without it. */
 int moe_stack_trace(void *device_buf, size_t bytes);
 int moe_stack_decode(const moe_pool_view *pool, const moe_geom *g, int32_t n_layers,
                      int32_t E, int32_t k, const uint16_t *x, const uint16_t *W,

@@ -212,14 +212,20 @@ class DecodeStack:
         g = self.geom.c_geom()
         b = self.bias.data_ptr() if self.bias is not None else None
         flags = _lib.MOE_STACK_ORDINARY if ordinary else _lib.MOE_STACK_COOPERATIVE
-        _lib.check(_lib.lib().moe_stack_decode(
-            C.byref(self.pool.c_view()), C.byref(g), self.L, self.E, self.k,
-            x_tok.data_ptr(), self.W.data_ptr(), b, self.geom.routing,
-            int(self.geom.norm_topk_prob), self.k_pred, self.table.data_ptr(),
-            self.p_y.data_ptr(), self.p_ids.data_ptr(), self.p_scores.data_ptr(),
-            self.p_refs.data_ptr(), self.p_pred.data_ptr(), self.p_miss.data_ptr(),
-            self.p_epoch, flags, self.p_ws.data_ptr(), self.p_ws.numel(),
-            _lib.stream_ptr(stream)))
+        try:
+            _lib.check(_lib.lib().moe_stack_decode(
+                C.byref(self.pool.c_view()), C.byref(g), self.L, self.E, self.k,
+                x_tok.data_ptr(), self.W.data_ptr(), b, self.geom.routing,
+                int(self.geom.norm_topk_prob), self.k_pred, self.table.data_ptr(),
+                self.p_y.data_ptr(), self.p_ids.data_ptr(), self.p_scores.data_ptr(),
+                self.p_refs.data_ptr(), self.p_pred.data_ptr(), self.p_miss.data_ptr(),
+                self.p_epoch, flags, self.p_ws.data_ptr(), self.p_ws.numel(),
+                _lib.stream_ptr(stream)))
+        except _lib.MoeError:
+            # nothing was launched: the counters still hold the previous
+            # epoch, which the next launch must follow
+            self.p_epoch -= 1
+            raise
 
     def check_persistent(self, stream=None):
         """Synchronise `stream` and read the device error word.  On an error

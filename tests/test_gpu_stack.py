@@ -238,3 +238,38 @@ def test_gptoss_persistent_lookahead_width_equals_per_layer(k_pred):
         assert torch.equal(st.p_y, y_ref), t
     del st
     torch.cuda.empty_cache()
+
+
+def test_phase_trace_leaves_outputs_unchanged(stack):
+    """moe_stack_trace: a traced launch gives the untraced outputs; each
+    traced workgroup stamps every layer's start in order and publishes its
+    down rows after the start; a buffer too small is refused; NULL ends it."""
+    from moe_stream_amd import _lib
+    L = _lib.lib()
+    xs = synth.hidden_states(1, stack.L, 2048, "cuda", 20260640)
+    stack.token_persistent(xs[0])
+    torch.cuda.synchronize()
+    y0 = stack.p_y.clone()
+    ids0 = stack.p_ids.clone()
+    buf = torch.zeros((256, stack.L, 15), dtype=torch.int64, device="cuda")
+    try:
+        _lib.check(L.moe_stack_trace(buf.data_ptr(), buf.numel() * 8 - 8))
+        with pytest.raises(_lib.MoeError):
+            stack.token_persistent(xs[0])
+        _lib.check(L.moe_stack_trace(buf.data_ptr(), buf.numel() * 8))
+        stack.token_persistent(xs[0])
+        torch.cuda.synchronize()
+        ops.check_device_error()
+    finally:
+        _lib.check(L.moe_stack_trace(None, 0))
+    assert torch.equal(stack.p_y, y0) and torch.equal(stack.p_ids, ids0)
+    tr = buf.cpu().numpy()
+    ran = tr[:, 0, 0] != 0
+    assert ran.sum() >= 128, ran.sum()
+    start, down = tr[ran, :, 0], tr[ran, :, 6]
+    assert np.all(start > 0) and np.all(np.diff(start, axis=1) >= 0)
+    assert np.all(down >= start)
+    assert start.max() - start.min() < 100_000_000   # within one second
+    stack.token_persistent(xs[0])                     # untraced again
+    torch.cuda.synchronize()
+    assert torch.equal(stack.p_y, y0)
