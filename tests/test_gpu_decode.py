@@ -211,3 +211,42 @@ def test_slot_lookup(qwen_layer):
     assert ei.value.code == _lib.MOE_ERR_DEVICE
     ops.check_device_error()   # cleared
     assert refs.cpu().tolist() == [table[3], 0, table[5]]
+
+
+def test_events_order_streams_and_time(qwen_layer):
+    """The event entry points as a caller orders slot reuse across streams
+    (needs_barrier, engine_v3.py:228-231): the block runs on a side stream
+    between two recorded events; the current stream waits on the second and
+    then reads the output, which equals the same block run in order; the
+    event reports done and a non-negative elapsed time."""
+    import ctypes as C
+    L = _lib.lib()
+    g = qwen_layer.geom
+    x = bf16_randn((1, 2048), seed=20260036)
+    bufs = ops.route(x, qwen_layer.W, None, g.routing, g.norm_topk_prob, g.top_k,
+                     table=qwen_layer.table)
+    ref = ops.ffn_decode(qwen_layer.pool, bufs.slot_refs, bufs.scores, x)
+    out = torch.zeros((1, 2048), dtype=torch.bfloat16, device="cuda")
+    ev0, ev1 = C.c_void_p(), C.c_void_p()
+    _lib.check(L.moe_event_create(C.byref(ev0)))
+    _lib.check(L.moe_event_create(C.byref(ev1)))
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        _lib.check(L.moe_event_record(ev0, side.cuda_stream))
+        ops.ffn_decode(qwen_layer.pool, bufs.slot_refs, bufs.scores, x, out=out, stream=side)
+        _lib.check(L.moe_event_record(ev1, side.cuda_stream))
+        _lib.check(L.moe_stream_wait_event(torch.cuda.current_stream().cuda_stream, ev1))
+        copy = out.clone()   # on the current stream, ordered after the block
+        torch.cuda.synchronize()
+        ops.check_device_error()
+        assert L.moe_event_query(ev1) == 1
+        ms = C.c_float(-1.0)
+        _lib.check(L.moe_event_elapsed_ms(ev0, ev1, C.byref(ms)))
+        assert 0.0 <= ms.value < 1000.0, ms.value
+        assert torch.equal(copy, ref)
+        with pytest.raises(_lib.MoeError):
+            _lib.check(L.moe_event_record(None, side.cuda_stream))
+    finally:
+        _lib.check(L.moe_event_destroy(ev0))
+        _lib.check(L.moe_event_destroy(ev1))
